@@ -1,0 +1,166 @@
+/* pulsar_moe.h - C ABI of the MI355X (gfx950) quantized expert-matvec library.
+ *
+ * Every entry point keeps the name, argument order, argument meaning and
+ * return convention of the reference kernel library it replaces, so the
+ * reference's Rust FFI block (crates/kernels/src/lib.rs:78-194) binds this
+ * library unchanged:
+ *   - return 1 on success, 0 on failure (invalid arguments or a launch error);
+ *     the reason is printed as "pulsar-kernels: <what>: <error>" on stderr
+ *     (crates/kernels/cuda/pulsar_kernels.cu:25-29);
+ *   - every pointer argument except the self-tests' is a DEVICE pointer the
+ *     caller owns; the library allocates nothing on these paths;
+ *   - launches are asynchronous on the calling thread's current default
+ *     stream (the null stream); nothing here synchronises.
+ *
+ * Byte layouts are the GGUF/ggml ones (crates/gguf/src/lib.rs:145-180):
+ *   Q2_K 84 B / 256, Q4_K 144 B / 256, Q6_K 210 B / 256, IQ2_XXS 66 B / 256,
+ *   MXFP4 17 B / 32 (rows pack whole 32-value blocks, not super-blocks),
+ *   q8_K 292 B / 256.
+ */
+#ifndef PULSAR_MOE_H
+#define PULSAR_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Quant codes (crates/kernels/src/lib.rs:55-73; pulsar_kernels.cu:2649-2668).
+ * This library implements the five expert formats of the hot path; the
+ * other reference codes (3, 5-11, 13-17) are rejected with a 0 return. */
+#define PULSAR_QUANT_Q2_K     0u
+#define PULSAR_QUANT_IQ2_XXS  1u
+#define PULSAR_QUANT_Q4_K     2u
+#define PULSAR_QUANT_Q6_K     4u
+#define PULSAR_QUANT_MXFP4   12u
+/* OR'd into `quant` by callers that permit W4A4 (crates/kernels/src/lib.rs:51-55);
+ * accepted and ignored here (it only selects an NVFP4 path in the reference). */
+#define PULSAR_QUANT_A4_OK   0x80000000u
+
+/* act_op codes of the gated combine (pulsar_kernels.cu:114-141) */
+#define PULSAR_ACT_SILU        0u /* silu(g) * u */
+#define PULSAR_ACT_SWIGLU_OAI  2u /* gpt-oss: clamp 7, alpha 1.702, (u + 1) */
+
+#define PULSAR_QK_K 256u
+
+/* q8_K activation block (pulsar_kernels.cu:1492-1496; lane Q8KRow,
+ * crates/quant/src/cpu_dot.rs:19-23): d at byte 0, qs at 4, bsums at 260. */
+typedef struct pulsar_block_q8_K {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+} pulsar_block_q8_K;
+
+/* Per-(token, slot) expert pointers (pulsar_kernels.cu:2555-2564;
+ * crates/kernels/src/lib.rs:21-49). A NULL gate or up makes the pair stage
+ * write 0 for that slot; a NULL down makes the down stage skip it; NULL
+ * biases are skipped. gate_b/up_b hold mid_dim floats, down_b out_dim. */
+typedef struct pulsar_expert_ptrs {
+    const void *gate;
+    const void *up;
+    const void *down;
+    const float *gate_b;
+    const float *up_b;
+    const float *down_b;
+} pulsar_expert_ptrs;
+
+#ifdef __cplusplus
+static_assert(sizeof(pulsar_block_q8_K) == 292, "block_q8_K is 292 bytes");
+static_assert(sizeof(pulsar_expert_ptrs) == 48, "pulsar_expert_ptrs is 48 bytes");
+#else
+_Static_assert(sizeof(pulsar_block_q8_K) == 292, "block_q8_K is 292 bytes");
+_Static_assert(sizeof(pulsar_expert_ptrs) == 48, "pulsar_expert_ptrs is 48 bytes");
+#endif
+
+/* f32 rows [n_rows][in_dim] -> q8_K rows [n_rows][ceil(in_dim/256)].
+ * Algorithm of the CPU lane (crates/quant/src/cpu_dot.rs:26-50): d = amax/127,
+ * q = clamp(round_half_away(x * (127/amax)), -127, 127), bsums = 16-sums;
+ * elements past in_dim in the tail block quantize to 0 (pulsar_kernels.cu:1499-1501).
+ * Replaces pulsar_quantize_q8_K (pulsar_kernels.cu:1552). */
+int pulsar_quantize_q8_K(void *out, const void *x, uint32_t in_dim, uint32_t n_rows);
+
+/* out[t][r] = sum_b dot(w row r block b, xq[t] block b), fp32 [n_tok][out_dim].
+ * quant in {Q2_K, IQ2_XXS, Q4_K, Q6_K}; in_dim % 256 == 0.
+ * Replaces pulsar_matmul_kq (pulsar_kernels.cu:4895). */
+int pulsar_matmul_kq(void *out, const void *w, const void *xq, uint32_t in_dim,
+                     uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes,
+                     uint32_t quant);
+
+/* mid[t][s][r] = glu(gate_r . x_t + gate_b[r], up_r . x_t + up_b[r], act_op) * weights[t][s].
+ * ptrs: pulsar_expert_ptrs[n_tok][n_used]; weights: f32 [n_tok][n_used];
+ * xq: q8_K [n_tok][ceil(in_dim/256)]. Replaces pulsar_moe_pair_swiglu
+ * (pulsar_kernels.cu:5149). */
+int pulsar_moe_pair_swiglu(void *mid, const void *ptrs, const void *weights,
+                           const void *xq, uint32_t in_dim, uint32_t mid_dim,
+                           uint32_t n_used, uint32_t n_tok, uint64_t row_bytes,
+                           uint32_t quant, uint32_t act_op);
+
+/* out[t][r] = sum_s down_r(slot s) . midq[t][s], fp32 [n_tok][out_dim];
+ * midq: q8_K [n_tok][n_used][ceil(mid_dim/256)]. Replaces pulsar_moe_down
+ * (pulsar_kernels.cu:5289). */
+int pulsar_moe_down(void *out, const void *ptrs, const void *midq,
+                    uint32_t mid_dim, uint32_t out_dim, uint32_t n_used,
+                    uint32_t n_tok, uint64_t row_bytes, uint32_t quant);
+
+/* Grouped (CSR by expert) pair stage: gptrs [n_group], starts [n_group+1],
+ * pairs [starts[n_group]] packing token << 4 | slot (n_used <= 16).
+ * Writes mid[t][s][r] for every listed pair. Replaces
+ * pulsar_moe_pair_swiglu_grouped (pulsar_kernels.cu:3483). */
+int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *starts,
+                                   const void *pairs, const void *weights,
+                                   const void *xq, uint32_t in_dim, uint32_t mid_dim,
+                                   uint32_t n_used, uint32_t n_group,
+                                   uint64_t row_bytes, uint32_t quant,
+                                   uint32_t act_op);
+
+/* Grouped down stage: partial[t][s][r] = down_r(group of (t,s)) . midq[t][s]
+ * for every listed pair; unlisted (t, s) are left untouched (the caller
+ * zeroes partial first). Replaces pulsar_moe_down_grouped (pulsar_kernels.cu:3537). */
+int pulsar_moe_down_grouped(void *partial, const void *gptrs, const void *starts,
+                            const void *pairs, const void *midq, uint32_t mid_dim,
+                            uint32_t out_dim, uint32_t n_used, uint32_t n_group,
+                            uint64_t row_bytes, uint32_t quant);
+
+/* out[t][r] = sum_s partial[t][s][r] in slot order. Replaces
+ * pulsar_moe_slot_sum (pulsar_kernels.cu:3651). */
+int pulsar_moe_slot_sum(void *out, const void *partial, uint32_t out_dim,
+                        uint32_t n_used, uint32_t n_tok);
+
+/* out[t][r] += sum_s weights[t][s] * down_b(slot s)[r] (slots with a NULL
+ * down_b skipped; nothing added where the sum is 0). Replaces
+ * pulsar_moe_down_bias (pulsar_kernels.cu:3640). */
+int pulsar_moe_down_bias(void *out, const void *ptrs, const void *weights,
+                         uint32_t out_dim, uint32_t n_used, uint32_t n_tok);
+
+/* Router top-k (pulsar_kernels.cu:938-1050): selected int32 and weights f32
+ * [n_tok][k_used(+n_shexp)] from logits f32 [n_tok][n_expert(+n_shexp)].
+ * mode 0 sigmoid + bias, normalised; mode 1 softmax over the k winners
+ * (selection on raw logit + bias); mode 2 sigmoid+bias selection with the
+ * shared "sink" logits appended, weights softmax(logsigmoid). Ties go to the
+ * lower expert index. n_expert(+n_shexp) <= 1024. Replaces
+ * pulsar_router_select (pulsar_kernels.cu:1052). */
+int pulsar_router_select(void *selected, void *weights, const void *logits,
+                         const void *bias, uint32_t n_expert, uint32_t k_used,
+                         float weight_scale, uint32_t n_tok, uint32_t softmax_mode,
+                         uint32_t n_shexp);
+
+/* out[t][o] = sum_i w[o][i] * x[t][i] in fp32 (router logits). Replaces
+ * pulsar_matmul_f32 (pulsar_kernels.cu:6526). */
+int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32_t in_dim,
+                      uint32_t out_dim, uint32_t n_tok);
+
+/* x[r][i] += bias[i] for rows rows of dim floats. Replaces
+ * pulsar_add_bias_rows (pulsar_kernels.cu:3631). */
+int pulsar_add_bias_rows(void *x, const void *bias, uint32_t dim, uint32_t rows);
+
+/* Streaming-read probe: reads `bytes` (a multiple of 16) from buf through
+ * the compute units; `sink` receives nothing unless the data sums to an
+ * impossible value. Replaces pulsar_bw_read (pulsar_kernels.cu:4889). */
+int pulsar_bw_read(void *buf, uint64_t bytes, void *sink);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PULSAR_MOE_H */

@@ -1,0 +1,851 @@
+/* pulsar_oracle.c - CPU restatement of the reference's quantized expert path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see pulsar_oracle.h): the checker for the HIP
+ * library and the CPU baseline that bench.py times. Build with
+ * -O2 -ffp-contract=off (oracle/Makefile).
+ *
+ * Reference files this follows (all paths under the reference checkout):
+ *   cpu   = crates/quant/src/cpu_dot.rs           (the CPU expert lane)
+ *   cu    = crates/kernels/cuda/pulsar_kernels.cu  (host mirrors, kernels)
+ *   elib  = crates/engine/src/lib.rs               (Lane composition)
+ */
+#include "pulsar_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../include/pulsar_iq2xxs_grid.h"
+
+/* ---------------------------------------------------------------- f16 -- */
+
+/* cpu:52-64 (exact, including subnormals) */
+float po_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    const uint32_t man = h & 0x3ffu;
+    uint32_t bits;
+    float f;
+    if (exp == 0) {
+        bits = sign | 0x38800000u; /* +-2^-14 */
+        memcpy(&f, &bits, 4);
+        return f * ((float)man / 1024.0f);
+    }
+    if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* crates/quant/src/lib.rs:51-82 (round to nearest even) */
+uint16_t po_f32_to_f16(float x) {
+    uint32_t bits;
+    memcpy(&bits, &x, 4);
+    const uint16_t s = (uint16_t)((bits >> 16) & 0x8000u);
+    const int32_t e = (int32_t)((bits >> 23) & 0xffu);
+    const uint32_t m = bits & 0x7fffffu;
+    if (e == 0xff) return (uint16_t)(s | 0x7c00u | (m ? 0x200u : 0u));
+    const int32_t e16 = e - 127 + 15;
+    if (e16 >= 0x1f) return (uint16_t)(s | 0x7c00u);
+    if (e16 <= 0) {
+        if (e16 < -10) return s;
+        const uint32_t mm = m | 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e16);
+        const uint32_t half = mm >> shift;
+        const uint32_t rem = mm & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1u);
+        const uint32_t rounded = half + ((rem > halfway) | ((rem == halfway) & (half & 1u)));
+        return (uint16_t)(s | rounded);
+    }
+    const uint32_t half = (uint32_t)s | ((uint32_t)e16 << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    const uint32_t rounded = half + ((rem > 0x1000u) | ((rem == 0x1000u) & (half & 1u)));
+    return (uint16_t)rounded;
+}
+
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+static inline uint32_t rd32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* --------------------------------------------------------------- q8_K -- */
+
+/* cpu:26-50. amax folds with max from 0; an all-zero block gets d = 0 and
+ * zero quants; otherwise d = amax/127, inv = 127/amax and
+ * q = clamp(round(x*inv), -127, 127) with round = half away from zero.
+ * The tail past in_dim is zero (cu:1499-1501), which leaves amax unchanged. */
+void po_quantize_q8_K(pulsar_block_q8_K *out, const float *x, uint32_t in_dim, uint32_t n_rows) {
+    const uint32_t nb = (in_dim + 255u) / 256u;
+    for (uint32_t r = 0; r < n_rows; r++) {
+        for (uint32_t b = 0; b < nb; b++) {
+            pulsar_block_q8_K *yb = out + (uint64_t)r * nb + b;
+            float v[256];
+            for (uint32_t i = 0; i < 256; i++) {
+                const uint64_t c = (uint64_t)b * 256u + i;
+                v[i] = c < in_dim ? x[(uint64_t)r * in_dim + c] : 0.0f;
+            }
+            float amax = 0.0f;
+            for (uint32_t i = 0; i < 256; i++) amax = fmaxf(amax, fabsf(v[i]));
+            if (amax == 0.0f) {
+                memset(yb, 0, sizeof(*yb));
+                continue;
+            }
+            const float scale = amax / 127.0f;
+            const float inv = 127.0f / amax;
+            yb->d = scale;
+            for (uint32_t i = 0; i < 256; i++) {
+                /* Rust's `f32 as i8` saturates and maps NaN to 0; NaN arises
+                 * only when 127/amax overflows (amax < ~3.7e-37) on a 0 */
+                float q = roundf(v[i] * inv);
+                if (q != q) q = 0.0f;
+                if (q < -127.0f) q = -127.0f;
+                if (q > 127.0f) q = 127.0f;
+                yb->qs[i] = (int8_t)q;
+            }
+            for (uint32_t g = 0; g < 16; g++) {
+                int32_t s = 0;
+                for (uint32_t i = 0; i < 16; i++) s += yb->qs[16 * g + i];
+                yb->bsums[g] = (int16_t)s;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------ formats -- */
+
+uint32_t po_sb_bytes(uint32_t quant) {
+    switch (quant) {
+    case PULSAR_QUANT_Q2_K: return 84;
+    case PULSAR_QUANT_IQ2_XXS: return 66;
+    case PULSAR_QUANT_Q4_K: return 144;
+    case PULSAR_QUANT_Q6_K: return 210;
+    case PULSAR_QUANT_MXFP4: return 8 * 17;
+    default: return 0;
+    }
+}
+
+/* crates/gguf/src/lib.rs:145-180: ceil(n / block) * block_bytes; MXFP4 is
+ * (32, 17), so its rows pack exact 32-value blocks. */
+uint64_t po_row_bytes(uint32_t quant, uint32_t n) {
+    if (quant == PULSAR_QUANT_MXFP4) return (uint64_t)((n + 31u) / 32u) * 17u;
+    return (uint64_t)((n + 255u) / 256u) * po_sb_bytes(quant);
+}
+
+/* cpu:147-156 == cu:1349-1359 (ggml get_scale_min_k4) */
+static void k4_scale_min(uint32_t j, const uint8_t *q, int32_t *sc, int32_t *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* IQ2_XXS grid, expanded from the base-3 codes of include/pulsar_iq2xxs_grid.h
+ * (digit d_j -> magnitude {8, 25, 43}[d_j] in byte j). */
+static const uint16_t k_iq2xxs_codes[256] = {PULSAR_IQ2XXS_GRID_CODES};
+static uint8_t iq2xxs_mag(uint32_t idx, uint32_t j) {
+    static const uint8_t mags[3] = {8, 25, 43};
+    uint32_t c = k_iq2xxs_codes[idx];
+    for (uint32_t k = 0; k < j; k++) c /= 3u;
+    return mags[c % 3u];
+}
+
+/* cpu:66-70: 7 stored sign bits, bit 7 completes even parity */
+static uint32_t sign_mask(uint32_t s7) {
+    return s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
+}
+
+/* cu:1424-1448: doubled E2M1 table and its compensating 2^(e-128) scale,
+ * flushed to zero for e < 2 */
+static const int32_t k_mxfp4_kv[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+static float mxfp4_scale_half(uint8_t e) {
+    if (e < 2) return 0.0f;
+    const uint32_t bits = (uint32_t)(e - 1u) << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+float po_block_dot(uint32_t quant, const uint8_t *row, uint32_t b,
+                   const pulsar_block_q8_K *y, uint32_t n_valid32,
+                   int32_t *i0, int32_t *i1, int32_t sumi_out[8]) {
+    const int8_t *q8 = y->qs;
+    const int16_t *bs = y->bsums;
+    const float yd = y->d;
+    int32_t d0 = 0, d1 = 0;
+    float f = 0.0f;
+    switch (quant) {
+    case PULSAR_QUANT_Q4_K: {
+        /* cpu:250-279 */
+        const uint8_t *blk = row + (uint64_t)b * 144u;
+        const float xd = po_f16_to_f32(rd16(blk));
+        const float xmin = po_f16_to_f32(rd16(blk + 2));
+        const uint8_t *scales = blk + 4;
+        const uint8_t *q4 = blk + 16;
+        int32_t isum = 0, msum = 0;
+        for (uint32_t j = 0; j < 4; j++) {
+            int32_t sc1, m1, sc2, m2;
+            k4_scale_min(2 * j, scales, &sc1, &m1);
+            k4_scale_min(2 * j + 1, scales, &sc2, &m2);
+            int32_t s1 = 0, s2 = 0;
+            for (uint32_t i = 0; i < 32; i++) {
+                const uint8_t v = q4[32 * j + i];
+                s1 += (int32_t)(v & 0x0f) * q8[64 * j + i];
+                s2 += (int32_t)(v >> 4) * q8[64 * j + 32 + i];
+            }
+            isum += sc1 * s1 + sc2 * s2;
+            msum += m1 * (bs[4 * j] + bs[4 * j + 1]) + m2 * (bs[4 * j + 2] + bs[4 * j + 3]);
+        }
+        d0 = isum;
+        d1 = msum;
+        f = xd * yd * (float)isum - xmin * yd * (float)msum;
+        break;
+    }
+    case PULSAR_QUANT_Q2_K: {
+        /* cpu:732-767 */
+        const uint8_t *blk = row + (uint64_t)b * 84u;
+        const uint8_t *sc = blk;
+        const uint8_t *q2 = blk + 16;
+        const float xd = po_f16_to_f32(rd16(blk + 80));
+        const float xmin = po_f16_to_f32(rd16(blk + 82));
+        int32_t summs = 0;
+        for (uint32_t j = 0; j < 16; j++) summs += bs[j] * (int32_t)(sc[j] >> 4);
+        int32_t isum = 0;
+        uint32_t is = 0;
+        for (uint32_t k = 0; k < 2; k++) {
+            for (uint32_t shift = 0; shift < 8; shift += 2) {
+                for (uint32_t half = 0; half < 2; half++) {
+                    const int32_t d = sc[is] & 0x0f;
+                    is++;
+                    int32_t sumi = 0;
+                    for (uint32_t i = 0; i < 16; i++) {
+                        const int32_t q = (q2[32 * k + 16 * half + i] >> shift) & 3;
+                        sumi += q * q8[128 * k + 32 * (shift / 2) + 16 * half + i];
+                    }
+                    isum += d * sumi;
+                }
+            }
+        }
+        d0 = isum;
+        d1 = summs;
+        f = yd * xd * (float)isum - yd * xmin * (float)summs;
+        break;
+    }
+    case PULSAR_QUANT_Q6_K: {
+        /* cu:5920-5948 (== cu:1830-1861, cu:3163-3188) */
+        const uint8_t *blk = row + (uint64_t)b * 210u;
+        const uint8_t *ql = blk;
+        const uint8_t *qh = blk + 128;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        const float xd = po_f16_to_f32(rd16(blk + 208));
+        int32_t isum = 0;
+        for (uint32_t j = 0; j < 2; j++) {
+            int32_t g[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (uint32_t i = 0; i < 32; i++) {
+                const uint32_t sub = i >> 4;
+                const int32_t v0 = ((ql[i] & 0x0f) | (((qh[i] >> 0) & 3) << 4)) - 32;
+                const int32_t v1 = ((ql[32 + i] & 0x0f) | (((qh[i] >> 2) & 3) << 4)) - 32;
+                const int32_t v2 = ((ql[i] >> 4) | (((qh[i] >> 4) & 3) << 4)) - 32;
+                const int32_t v3 = ((ql[32 + i] >> 4) | (((qh[i] >> 6) & 3) << 4)) - 32;
+                g[0 + sub] += v0 * q8[i];
+                g[2 + sub] += v1 * q8[32 + i];
+                g[4 + sub] += v2 * q8[64 + i];
+                g[6 + sub] += v3 * q8[96 + i];
+            }
+            for (uint32_t k = 0; k < 8; k++) isum += (int32_t)sc[k] * g[k];
+            sc += 8;
+            ql += 64;
+            qh += 32;
+            q8 += 128;
+        }
+        d0 = isum;
+        f = xd * yd * (float)isum;
+        break;
+    }
+    case PULSAR_QUANT_IQ2_XXS: {
+        /* cpu:92-122 */
+        const uint8_t *blk = row + (uint64_t)b * 66u;
+        const float xd = po_f16_to_f32(rd16(blk));
+        int32_t bsum = 0;
+        for (uint32_t ib32 = 0; ib32 < 8; ib32++) {
+            const uint32_t aux0 = rd32(blk + 2 + 8 * ib32);
+            const uint32_t aux1 = rd32(blk + 6 + 8 * ib32);
+            const int32_t ls = (int32_t)(2u * (aux1 >> 28) + 1u);
+            int32_t sumi = 0;
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t gi = (aux0 >> (8 * k)) & 0xffu;
+                const uint32_t sm = sign_mask((aux1 >> (7 * k)) & 127u);
+                for (uint32_t i = 0; i < 8; i++) {
+                    const int32_t g = iq2xxs_mag(gi, i);
+                    const int32_t w = ((sm >> i) & 1u) ? -g : g;
+                    sumi += w * q8[32 * ib32 + 8 * k + i];
+                }
+            }
+            bsum += sumi * ls;
+        }
+        d0 = bsum;
+        f = 0.125f * xd * yd * (float)bsum;
+        break;
+    }
+    case PULSAR_QUANT_MXFP4: {
+        /* cu:5715-5741; blocks past the row's last valid 32-block are not
+         * read (their activations are the zero-padded q8_K tail, so the
+         * reference's sumi == 0 skip drops them anyway) */
+        const uint8_t *base = row + (uint64_t)b * 136u;
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 8; k++) {
+            int32_t sumi = 0;
+            if (k < n_valid32) {
+                const uint8_t *bp = base + 17u * k;
+                for (uint32_t i = 0; i < 16; i++) {
+                    const uint8_t q = bp[1 + i];
+                    sumi += k_mxfp4_kv[q & 0x0f] * q8[32 * k + i];
+                    sumi += k_mxfp4_kv[q >> 4] * q8[32 * k + 16 + i];
+                }
+                if (sumi != 0) sumf += mxfp4_scale_half(bp[0]) * (float)sumi;
+            }
+            if (sumi_out) sumi_out[k] = sumi;
+        }
+        f = yd * sumf;
+        break;
+    }
+    default:
+        break;
+    }
+    if (i0) *i0 = d0;
+    if (i1) *i1 = d1;
+    return f;
+}
+
+static uint32_t valid32_in_sb(uint32_t n, uint32_t b) {
+    const uint32_t rem = n - 256u * b;
+    return rem >= 256u ? 8u : (rem + 31u) / 32u;
+}
+
+/* cpu:242-279 (and siblings): total = 0; total += f_b for b in order */
+float po_vec_dot(uint32_t quant, const uint8_t *row, const pulsar_block_q8_K *xq,
+                 uint32_t n, double *abs_sum) {
+    const uint32_t nb = (n + 255u) / 256u;
+    float total = 0.0f;
+    double as = 0.0;
+    for (uint32_t b = 0; b < nb; b++) {
+        const float f = po_block_dot(quant, row, b, xq + b, valid32_in_sb(n, b), NULL, NULL, NULL);
+        total += f;
+        as += fabs((double)f);
+    }
+    if (abs_sum) *abs_sum = as;
+    return total;
+}
+
+/* f64 element-wise dequant, straight from the format descriptions (the
+ * reference tests' dequant references: cpu:848-872, 925-947, 971-989). */
+void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out) {
+    const uint32_t nb = (n + 255u) / 256u;
+    for (uint32_t b = 0; b < nb; b++) {
+        double v[256];
+        memset(v, 0, sizeof(v));
+        switch (quant) {
+        case PULSAR_QUANT_Q4_K: {
+            const uint8_t *blk = row + (uint64_t)b * 144u;
+            const double xd = po_f16_to_f32(rd16(blk));
+            const double xmin = po_f16_to_f32(rd16(blk + 2));
+            for (uint32_t s = 0; s < 8; s++) { /* sub-block s: values 32s.. */
+                int32_t sc, m;
+                k4_scale_min(s, blk + 4, &sc, &m);
+                for (uint32_t i = 0; i < 32; i++) {
+                    const uint8_t byte = blk[16 + 32 * (s / 2) + i];
+                    const int32_t q = (s & 1) ? (byte >> 4) : (byte & 0x0f);
+                    v[32 * s + i] = xd * sc * q - xmin * m;
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_Q2_K: {
+            const uint8_t *blk = row + (uint64_t)b * 84u;
+            const double xd = po_f16_to_f32(rd16(blk + 80));
+            const double xmin = po_f16_to_f32(rd16(blk + 82));
+            for (uint32_t c = 0; c < 16; c++) { /* 16-value chunk c (cpu:852-872) */
+                const uint32_t k = c / 8, js = (c % 8) / 2, half = c % 2;
+                for (uint32_t i = 0; i < 16; i++) {
+                    const int32_t q = (blk[16 + 32 * k + 16 * half + i] >> (2 * js)) & 3;
+                    v[16 * c + i] = xd * (blk[c] & 0x0f) * q - xmin * (blk[c] >> 4);
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_Q6_K: {
+            /* value 128h + 32q + i (h half, q quarter): low 4 bits from
+             * ql[64h + 32(q&1) + i] nibble q>>1, high 2 from qh[32h + i]
+             * bits 2q..2q+1, minus 32; scale sc[8h + (32q + i)/16] */
+            const uint8_t *blk = row + (uint64_t)b * 210u;
+            const double xd = po_f16_to_f32(rd16(blk + 208));
+            const int8_t *sc = (const int8_t *)(blk + 192);
+            for (uint32_t h = 0; h < 2; h++)
+                for (uint32_t q = 0; q < 4; q++)
+                    for (uint32_t i = 0; i < 32; i++) {
+                        const uint8_t lb = blk[64 * h + 32 * (q & 1) + i];
+                        const int32_t lo = (q >> 1) ? (lb >> 4) : (lb & 0x0f);
+                        const int32_t hi = (blk[128 + 32 * h + i] >> (2 * q)) & 3;
+                        const uint32_t vi = 32 * q + i;
+                        v[128 * h + vi] = xd * sc[8 * h + vi / 16] * ((lo | (hi << 4)) - 32);
+                    }
+            break;
+        }
+        case PULSAR_QUANT_IQ2_XXS: {
+            const uint8_t *blk = row + (uint64_t)b * 66u;
+            const double xd = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++) {
+                const uint32_t aux0 = rd32(blk + 2 + 8 * g);
+                const uint32_t aux1 = rd32(blk + 6 + 8 * g);
+                const double db = 0.125 * xd * (2.0 * (aux1 >> 28) + 1.0);
+                for (uint32_t k = 0; k < 4; k++) {
+                    const uint32_t sm = sign_mask((aux1 >> (7 * k)) & 127u);
+                    for (uint32_t i = 0; i < 8; i++) {
+                        const double mag = iq2xxs_mag((aux0 >> (8 * k)) & 0xffu, i);
+                        v[32 * g + 8 * k + i] = ((sm >> i) & 1u) ? -db * mag : db * mag;
+                    }
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_MXFP4: {
+            /* textbook OCP MX: value = E2M1(code) * 2^(e - 127), E2M1
+             * magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6}, bit 3 = sign
+             * (crates/gguf/src/lib.rs:73-76); the reference flushes e < 2 */
+            static const double e2m1[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+            const uint32_t nv = valid32_in_sb(n, b);
+            for (uint32_t k = 0; k < nv; k++) {
+                const uint8_t *bp = row + (uint64_t)b * 136u + 17u * k;
+                const double scale = bp[0] < 2 ? 0.0 : ldexp(1.0, (int)bp[0] - 127);
+                for (uint32_t i = 0; i < 16; i++) {
+                    const uint8_t lo = bp[1 + i] & 0x0f, hi = bp[1 + i] >> 4;
+                    v[32 * k + i] = (lo & 8 ? -1.0 : 1.0) * e2m1[lo & 7] * scale;
+                    v[32 * k + 16 + i] = (hi & 8 ? -1.0 : 1.0) * e2m1[hi & 7] * scale;
+                }
+            }
+            break;
+        }
+        default:
+            break;
+        }
+        for (uint32_t i = 0; i < 256; i++) {
+            const uint64_t c = (uint64_t)b * 256u + i;
+            if (c < n) out[c] = v[i];
+        }
+    }
+}
+
+static int quant_ok(uint32_t quant) {
+    return quant == PULSAR_QUANT_Q2_K || quant == PULSAR_QUANT_IQ2_XXS ||
+           quant == PULSAR_QUANT_Q4_K || quant == PULSAR_QUANT_Q6_K ||
+           quant == PULSAR_QUANT_MXFP4;
+}
+
+/* cu:4895-4906 argument contract; each output is the lane's row dot */
+int po_matmul_kq(float *out, const uint8_t *w, const pulsar_block_q8_K *xq,
+                 uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
+                 uint64_t row_bytes, uint32_t quant) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    if (in_dim == 0 || in_dim % 256u != 0 || out_dim == 0 || n_tok == 0 || row_bytes == 0 ||
+        quant == PULSAR_QUANT_MXFP4 || !quant_ok(quant))
+        return 0;
+    const uint32_t nb = in_dim / 256u;
+    for (uint32_t t = 0; t < n_tok; t++)
+        for (uint32_t r = 0; r < out_dim; r++)
+            out[(uint64_t)t * out_dim + r] =
+                po_vec_dot(quant, w + (uint64_t)r * row_bytes, xq + (uint64_t)t * nb, in_dim, NULL);
+    return 1;
+}
+
+/* ---------------------------------------------------------------- glu -- */
+
+/* cu:124-141 == elib:2131-2157 */
+float po_glu(float g, float u, uint32_t op) {
+    if (op == 2u) {
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -7.0f), 7.0f);
+        return g / (1.0f + expf(-1.702f * g)) * (u + 1.0f);
+    }
+    return g / (1.0f + expf(-g)) * u;
+}
+
+/* ---------------------------------------------------------------- MoE -- */
+
+/* cu:2566-2614 semantics with the lane's per-row sequential dots
+ * (elib:2042-2050): NULL gate/up -> 0; bias added to the projection output
+ * before the combine; router weight multiplies the combine. */
+int po_moe_pair_swiglu(float *mid, const pulsar_expert_ptrs *ptrs, const float *weights,
+                       const pulsar_block_q8_K *xq, uint32_t in_dim, uint32_t mid_dim,
+                       uint32_t n_used, uint32_t n_tok, uint64_t row_bytes,
+                       uint32_t quant, uint32_t act_op) {
+    if (in_dim == 0 || mid_dim == 0 || n_used == 0 || n_tok == 0 || row_bytes == 0 ||
+        !quant_ok(quant) || (act_op != 0u && act_op != 2u))
+        return 0;
+    const uint32_t nb = (in_dim + 255u) / 256u;
+    for (uint32_t t = 0; t < n_tok; t++) {
+        for (uint32_t s = 0; s < n_used; s++) {
+            const uint64_t so = (uint64_t)t * n_used + s;
+            const pulsar_expert_ptrs p = ptrs[so];
+            float *m = mid + so * mid_dim;
+            if (!p.gate || !p.up) {
+                memset(m, 0, (size_t)mid_dim * 4u);
+                continue;
+            }
+            for (uint32_t r = 0; r < mid_dim; r++) {
+                float g = po_vec_dot(quant, (const uint8_t *)p.gate + (uint64_t)r * row_bytes,
+                                     xq + (uint64_t)t * nb, in_dim, NULL);
+                float u = po_vec_dot(quant, (const uint8_t *)p.up + (uint64_t)r * row_bytes,
+                                     xq + (uint64_t)t * nb, in_dim, NULL);
+                if (p.gate_b) g += p.gate_b[r];
+                if (p.up_b) u += p.up_b[r];
+                m[r] = po_glu(g, u, act_op) * weights[so];
+            }
+        }
+    }
+    return 1;
+}
+
+/* cu:2616-2647 semantics in the lane's form (elib:2086-2093): per output
+ * row, the slots' full row dots summed in slot order; NULL down skipped. */
+int po_moe_down(float *out, const pulsar_expert_ptrs *ptrs, const pulsar_block_q8_K *midq,
+                uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint32_t n_tok,
+                uint64_t row_bytes, uint32_t quant) {
+    if (mid_dim == 0 || out_dim == 0 || n_used == 0 || n_tok == 0 || row_bytes == 0 ||
+        !quant_ok(quant))
+        return 0;
+    const uint32_t mb = (mid_dim + 255u) / 256u;
+    for (uint32_t t = 0; t < n_tok; t++) {
+        for (uint32_t r = 0; r < out_dim; r++) {
+            float sum = 0.0f;
+            for (uint32_t s = 0; s < n_used; s++) {
+                const uint64_t so = (uint64_t)t * n_used + s;
+                const pulsar_expert_ptrs p = ptrs[so];
+                if (!p.down) continue;
+                sum += po_vec_dot(quant, (const uint8_t *)p.down + (uint64_t)r * row_bytes,
+                                  midq + so * mb, mid_dim, NULL);
+            }
+            out[(uint64_t)t * out_dim + r] = sum;
+        }
+    }
+    return 1;
+}
+
+/* cu:3601-3619 */
+int po_moe_down_bias(float *out, const pulsar_expert_ptrs *ptrs, const float *weights,
+                     uint32_t out_dim, uint32_t n_used, uint32_t n_tok) {
+    if (out_dim == 0 || n_used == 0 || n_tok == 0) return 0;
+    for (uint32_t t = 0; t < n_tok; t++)
+        for (uint32_t r = 0; r < out_dim; r++) {
+            float b = 0.0f;
+            for (uint32_t s = 0; s < n_used; s++) {
+                const uint64_t so = (uint64_t)t * n_used + s;
+                if (ptrs[so].down_b) b += weights[so] * ptrs[so].down_b[r];
+            }
+            if (b != 0.0f) out[(uint64_t)t * out_dim + r] += b;
+        }
+    return 1;
+}
+
+/* ------------------------------------------------------------- router -- */
+
+/* cu:6504-6535 contract; the sum here is sequential in f64 (the kernel's
+ * tree order differs; tests compare within a stated tolerance) */
+int po_matmul_f32(float *out, const float *w, const float *x, uint32_t in_dim,
+                  uint32_t out_dim, uint32_t n_tok) {
+    if (in_dim == 0 || out_dim == 0 || n_tok == 0) return 0;
+    for (uint32_t t = 0; t < n_tok; t++)
+        for (uint32_t o = 0; o < out_dim; o++) {
+            double s = 0.0;
+            for (uint32_t i = 0; i < in_dim; i++)
+                s += (double)w[(uint64_t)o * in_dim + i] * (double)x[(uint64_t)t * in_dim + i];
+            out[(uint64_t)t * out_dim + o] = (float)s;
+        }
+    return 1;
+}
+
+/* cu:3621-3638 */
+int po_add_bias_rows(float *x, const float *bias, uint32_t dim, uint32_t rows) {
+    if (dim == 0 || rows == 0) return 0;
+    for (uint64_t i = 0; i < (uint64_t)rows * dim; i++) x[i] += bias[i % dim];
+    return 1;
+}
+
+/* cu:913-921 */
+static float router_sigmoid(float x) {
+    if (x >= 0.0f) {
+        const float e = expf(-x);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+/* cu:938-1050 (kernel semantics) with the contract of cu:1052-1064 */
+int po_router_select(int32_t *selected, float *weights, const float *logits,
+                     const float *bias, uint32_t n_expert, uint32_t k_used,
+                     float weight_scale, uint32_t n_tok, uint32_t mode, uint32_t n_shexp) {
+    if (n_expert == 0 || k_used == 0 || k_used > n_expert || n_tok == 0 ||
+        (mode != 2u && n_shexp != 0) || n_expert + (mode == 2u ? n_shexp : 0u) > 1024u)
+        return 0;
+    const uint32_t sink = mode == 2u ? n_shexp : 0u;
+    const uint32_t n_logit = n_expert + sink, n_slot = k_used + sink;
+    float *prob = (float *)malloc(n_expert * sizeof(float));
+    float *score = (float *)malloc(n_expert * sizeof(float));
+    for (uint32_t t = 0; t < n_tok; t++) {
+        const float *lg = logits + (uint64_t)t * n_logit;
+        int32_t *sel = selected + (uint64_t)t * n_slot;
+        float *w = weights + (uint64_t)t * n_slot;
+        for (uint32_t e = 0; e < n_expert; e++) {
+            const float raw = lg[e];
+            const float p = mode == 1u ? raw : router_sigmoid(raw);
+            prob[e] = mode == 2u ? raw : p;
+            score[e] = p + (bias ? bias[e] : 0.0f);
+        }
+        float sum = 0.0f;
+        for (uint32_t k = 0; k < k_used; k++) {
+            /* cu:922-925 comparator: higher score wins, ties go to the
+             * lower index, starting from (-inf, UINT32_MAX) */
+            uint32_t best = UINT32_MAX;
+            float best_score = -INFINITY;
+            for (uint32_t e = 0; e < n_expert; e++) {
+                if (score[e] > best_score || (score[e] == best_score && e < best)) {
+                    best_score = score[e];
+                    best = e;
+                }
+            }
+            if (best == UINT32_MAX) best = 0; /* all-NaN scores */
+            sel[k] = (int32_t)best;
+            w[k] = prob[best];
+            sum += prob[best];
+            score[best] = -INFINITY;
+        }
+        if (mode == 2u) {
+            for (uint32_t s = 0; s < sink; s++) {
+                sel[k_used + s] = (int32_t)(n_expert + s);
+                w[k_used + s] = lg[n_expert + s];
+            }
+            float m = -INFINITY;
+            for (uint32_t k = 0; k < n_slot; k++) {
+                const float x = w[k];
+                w[k] = x < 0.0f ? x - log1pf(expf(x)) : -log1pf(expf(-x));
+                m = fmaxf(m, w[k]);
+            }
+            float es = 0.0f;
+            for (uint32_t k = 0; k < n_slot; k++) {
+                w[k] = expf(w[k] - m);
+                es += w[k];
+            }
+            for (uint32_t k = 0; k < n_slot; k++) w[k] = w[k] / es * weight_scale;
+        } else if (mode == 1u) {
+            float m = -INFINITY;
+            for (uint32_t k = 0; k < k_used; k++) m = fmaxf(m, w[k]);
+            float es = 0.0f;
+            for (uint32_t k = 0; k < k_used; k++) {
+                w[k] = expf(w[k] - m);
+                es += w[k];
+            }
+            for (uint32_t k = 0; k < k_used; k++) w[k] = w[k] / es * weight_scale;
+        } else {
+            sum = fmaxf(sum, 6.103515625e-5f);
+            for (uint32_t k = 0; k < k_used; k++) w[k] = w[k] / sum * weight_scale;
+        }
+    }
+    free(prob);
+    free(score);
+    return 1;
+}
+
+/* --------------------------------------------------------------- LCG --- */
+
+float po_lcg(uint64_t *state) {
+    *state = *state * 6364136223846793005ull + 1442695040888963407ull;
+    return ((float)(*state >> 33) / (float)(1ull << 31)) - 1.0f;
+}
+
+/* ------------------------------------------------------ threaded lane -- */
+
+/* A persistent worker pool (the Lane's Pool, elib:1883-1930): jobs are
+ * claimed from an atomic counter; the caller joins on completion. */
+typedef void (*po_job_fn)(void *ctx, uint32_t job);
+
+typedef struct {
+    pthread_mutex_t mu;
+    pthread_cond_t cv_start, cv_done;
+    uint32_t n_threads;
+    uint64_t generation;
+    po_job_fn fn;
+    void *ctx;
+    uint32_t n_jobs;
+    uint32_t next_job;
+    uint32_t active;
+    pthread_t *tids;
+} po_pool;
+
+static po_pool g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER,
+                         PTHREAD_COND_INITIALIZER, 0, 0, NULL, NULL, 0, 0, 0, NULL};
+
+static void *pool_worker(void *arg) {
+    (void)arg;
+    uint64_t seen = 0;
+    pthread_mutex_lock(&g_pool.mu);
+    for (;;) {
+        while (g_pool.generation == seen) pthread_cond_wait(&g_pool.cv_start, &g_pool.mu);
+        seen = g_pool.generation;
+        g_pool.active++;
+        for (;;) {
+            if (g_pool.next_job >= g_pool.n_jobs) break;
+            const uint32_t j = g_pool.next_job++;
+            po_job_fn fn = g_pool.fn;
+            void *ctx = g_pool.ctx;
+            pthread_mutex_unlock(&g_pool.mu);
+            fn(ctx, j);
+            pthread_mutex_lock(&g_pool.mu);
+        }
+        g_pool.active--;
+        if (g_pool.active == 0) pthread_cond_broadcast(&g_pool.cv_done);
+    }
+    return NULL;
+}
+
+static void pool_run(uint32_t threads, po_job_fn fn, void *ctx, uint32_t n_jobs) {
+    if (threads <= 1 || n_jobs <= 1) {
+        for (uint32_t j = 0; j < n_jobs; j++) fn(ctx, j);
+        return;
+    }
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.n_threads < threads) {
+        g_pool.tids = (pthread_t *)realloc(g_pool.tids, (g_pool.n_threads + 1) * sizeof(pthread_t));
+        pthread_create(&g_pool.tids[g_pool.n_threads], NULL, pool_worker, NULL);
+        pthread_detach(g_pool.tids[g_pool.n_threads]);
+        g_pool.n_threads++;
+    }
+    g_pool.fn = fn;
+    g_pool.ctx = ctx;
+    g_pool.n_jobs = n_jobs;
+    g_pool.next_job = 0;
+    g_pool.generation++;
+    pthread_cond_broadcast(&g_pool.cv_start);
+    /* wait until every job is claimed and every worker that woke is idle */
+    while (g_pool.next_job < g_pool.n_jobs || g_pool.active > 0)
+        pthread_cond_wait(&g_pool.cv_done, &g_pool.mu);
+    pthread_mutex_unlock(&g_pool.mu);
+}
+
+typedef struct {
+    float *out;
+    const uint8_t *w;
+    const pulsar_block_q8_K *xq;
+    uint32_t in_dim, out_dim, n_tok, quant;
+    uint64_t row_bytes;
+} mv_ctx;
+
+static void mv_job(void *vctx, uint32_t job) {
+    const mv_ctx *c = (const mv_ctx *)vctx;
+    const uint32_t nb = (c->in_dim + 255u) / 256u;
+    const uint32_t lo = job * 256u;
+    const uint32_t hi = lo + 256u < c->out_dim ? lo + 256u : c->out_dim;
+    for (uint32_t r = lo; r < hi; r++)
+        for (uint32_t t = 0; t < c->n_tok; t++)
+            c->out[(uint64_t)t * c->out_dim + r] = po_vec_dot(
+                    c->quant, c->w + (uint64_t)r * c->row_bytes, c->xq + (uint64_t)t * nb, c->in_dim, NULL);
+}
+
+int po_matmul_kq_mt(float *out, const uint8_t *w, const pulsar_block_q8_K *xq,
+                    uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
+                    uint64_t row_bytes, uint32_t quant, uint32_t threads) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    if (in_dim == 0 || in_dim % 256u != 0 || out_dim == 0 || n_tok == 0 || row_bytes == 0 ||
+        !quant_ok(quant) || quant == PULSAR_QUANT_MXFP4)
+        return 0;
+    mv_ctx c = {out, w, xq, in_dim, out_dim, n_tok, quant, row_bytes};
+    pool_run(threads, mv_job, &c, (out_dim + 255u) / 256u);
+    return 1;
+}
+
+/* Lane stage A job: rows [lo, hi) of one (token, slot) pair's gate/up
+ * (elib:2037-2053), stage B job: rows [lo, hi) of one token's down sum over
+ * its slots (elib:2078-2096). */
+typedef struct {
+    const pulsar_expert_ptrs *ptrs;
+    const float *weights;
+    const pulsar_block_q8_K *xq, *midq;
+    float *mid, *out;
+    uint32_t in_dim, mid_dim, out_dim, n_used, n_tok, gq, dq, act_op;
+    uint64_t grb, drb;
+    uint32_t jobs_per_pair, jobs_per_tok;
+} lane_ctx;
+
+static void lane_a_job(void *vctx, uint32_t job) {
+    const lane_ctx *c = (const lane_ctx *)vctx;
+    const uint32_t so = job / c->jobs_per_pair;
+    const uint32_t lo = (job % c->jobs_per_pair) * 256u;
+    const uint32_t hi = lo + 256u < c->mid_dim ? lo + 256u : c->mid_dim;
+    const uint32_t t = so / c->n_used;
+    const uint32_t nb = (c->in_dim + 255u) / 256u;
+    const pulsar_expert_ptrs p = c->ptrs[so];
+    float *m = c->mid + (uint64_t)so * c->mid_dim;
+    for (uint32_t r = lo; r < hi; r++) {
+        if (!p.gate || !p.up) {
+            m[r] = 0.0f;
+            continue;
+        }
+        float g = po_vec_dot(c->gq, (const uint8_t *)p.gate + (uint64_t)r * c->grb,
+                             c->xq + (uint64_t)t * nb, c->in_dim, NULL);
+        float u = po_vec_dot(c->gq, (const uint8_t *)p.up + (uint64_t)r * c->grb,
+                             c->xq + (uint64_t)t * nb, c->in_dim, NULL);
+        if (p.gate_b) g += p.gate_b[r];
+        if (p.up_b) u += p.up_b[r];
+        m[r] = po_glu(g, u, c->act_op) * c->weights[so];
+    }
+}
+
+static void lane_b_job(void *vctx, uint32_t job) {
+    const lane_ctx *c = (const lane_ctx *)vctx;
+    const uint32_t t = job / c->jobs_per_tok;
+    const uint32_t lo = (job % c->jobs_per_tok) * 512u;
+    const uint32_t hi = lo + 512u < c->out_dim ? lo + 512u : c->out_dim;
+    const uint32_t mb = (c->mid_dim + 255u) / 256u;
+    for (uint32_t r = lo; r < hi; r++) {
+        float sum = 0.0f;
+        for (uint32_t s = 0; s < c->n_used; s++) {
+            const uint64_t so = (uint64_t)t * c->n_used + s;
+            const pulsar_expert_ptrs p = c->ptrs[so];
+            if (!p.down) continue;
+            sum += po_vec_dot(c->dq, (const uint8_t *)p.down + (uint64_t)r * c->drb,
+                              c->midq + so * mb, c->mid_dim, NULL);
+        }
+        c->out[(uint64_t)t * c->out_dim + r] = sum;
+    }
+}
+
+int po_lane_moe(float *out, const pulsar_expert_ptrs *ptrs, const float *weights,
+                const float *x, uint32_t in_dim, uint32_t mid_dim, uint32_t out_dim,
+                uint32_t n_used, uint32_t n_tok, uint64_t gate_row_bytes,
+                uint32_t gate_quant, uint64_t down_row_bytes, uint32_t down_quant,
+                uint32_t act_op, uint32_t threads) {
+    if (in_dim == 0 || mid_dim == 0 || out_dim == 0 || n_used == 0 || n_tok == 0 ||
+        !quant_ok(gate_quant) || !quant_ok(down_quant))
+        return 0;
+    const uint32_t nb = (in_dim + 255u) / 256u, mb = (mid_dim + 255u) / 256u;
+    pulsar_block_q8_K *xq = (pulsar_block_q8_K *)malloc((size_t)n_tok * nb * sizeof(pulsar_block_q8_K));
+    pulsar_block_q8_K *midq =
+            (pulsar_block_q8_K *)malloc((size_t)n_tok * n_used * mb * sizeof(pulsar_block_q8_K));
+    float *mid = (float *)malloc((size_t)n_tok * n_used * mid_dim * sizeof(float));
+    po_quantize_q8_K(xq, x, in_dim, n_tok);
+    lane_ctx c = {ptrs, weights, xq, midq, mid, out, in_dim, mid_dim, out_dim, n_used, n_tok,
+                  gate_quant, down_quant, act_op, gate_row_bytes, down_row_bytes,
+                  (mid_dim + 255u) / 256u, (out_dim + 511u) / 512u};
+    pool_run(threads, lane_a_job, &c, n_tok * n_used * c.jobs_per_pair);
+    po_quantize_q8_K(midq, mid, mid_dim, n_tok * n_used);
+    pool_run(threads, lane_b_job, &c, n_tok * c.jobs_per_tok);
+    free(xq);
+    free(midq);
+    free(mid);
+    return 1;
+}

@@ -1,0 +1,75 @@
+"""Builds libpulsar_moe.so (the HIP kernels + C ABI) in-tree for gfx950.
+
+    python -m pulsar_amd.build
+
+Each .hip translation unit compiles in parallel to an object under
+pulsar_amd/_build/, then the objects link into pulsar_amd/libpulsar_moe.so.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libpulsar_moe.so"
+SOURCES = ["q8k.hip", "matvec.hip", "moe.hip", "router.hip"]
+ARCH = os.environ.get("PULSAR_OFFLOAD_ARCH", "gfx950")
+
+# -ffp-contract=off: fp32 epilogues must round in source order (the reference
+#   CPU lane never fuses a*b+c).
+# -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 emitted by the compiler.
+# -mcode-object-version=5: loadable by the HIP runtime torch bundles.
+HIPFLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libpulsar_moe.so)")
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPFLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n" + "\n".join(noise))
+    if noise:
+        sys.stderr.write("\n".join(noise) + "\n")
+
+
+def build_library(jobs: int | None = None) -> Path:
+    """Compiles every HIP source and links libpulsar_moe.so; returns its path."""
+    BUILD.mkdir(exist_ok=True)
+    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
+    with ThreadPoolExecutor(max_workers=jobs or min(8, len(SOURCES))) as ex:
+        list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("link of libpulsar_moe.so failed:\n" + res.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build_library())

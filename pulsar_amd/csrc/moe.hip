@@ -1,0 +1,402 @@
+// moe.hip - routed-expert FFN stages on q8_K activations.
+//
+// Plain path (per (token, slot) expert pointers, pulsar_kernels.cu:2566-2647):
+//   pair : one block per (row group, slot, token); each wave streams the
+//          gate and the up rows of its rows once and applies the combine
+//          and the router weight;
+//   down : one block per (row group, token); the block's 4 waves split the
+//          token's slots, each slot's row dot lands in LDS and the slots
+//          are summed in slot order.
+// Grouped path (CSR by expert, pulsar_kernels.cu:2689-2789): one block per
+// (row group, expert group); the rows' weight units are loaded once into
+// registers and every (token, slot) pair of the group is dotted against them.
+#include "pk_rowdot.h"
+
+namespace pk {
+
+constexpr uint32_t kWaves = 4;      // waves per block
+constexpr uint32_t kSlotChunk = 32; // down-stage slots staged in LDS per round
+
+#define PK_IQ2_LUT(Q)                                               \
+    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? 256 : 1];    \
+    if ((Q) == PULSAR_QUANT_IQ2_XXS) {                              \
+        fill_iq2xxs_lut(lut);                                       \
+        __syncthreads();                                            \
+    }
+
+template <uint32_t Q, uint32_t UPLMAX>
+__global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
+                                                       const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                       const float *__restrict__ weights,
+                                                       const pulsar_block_q8_K *__restrict__ xq,
+                                                       uint32_t n_units, uint32_t nblk32,
+                                                       uint32_t lpr_log2, uint32_t in_blocks,
+                                                       uint32_t mid_dim, uint32_t n_used,
+                                                       uint64_t row_bytes, uint32_t act_op) {
+    PK_IQ2_LUT(Q)
+    const uint32_t slot = blockIdx.y, token = blockIdx.z;
+    const uint64_t so = (uint64_t)token * n_used + slot;
+    const pulsar_expert_ptrs p = ptrs[so];
+    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> lpr_log2;
+    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
+    const bool row_ok = row < mid_dim;
+    if (!p.gate || !p.up) {  // unrouted slot contributes zero (pulsar_kernels.cu:2587-2590)
+        if (row_ok && rg.lir == 0) mid[so * mid_dim + row] = 0.0f;
+        return;
+    }
+    Act a[UPLMAX];
+    load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
+    typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)row * row_bytes, row_ok, rg, wg);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)row * row_bytes, row_ok, rg, wu);
+    float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
+    float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
+    if (row_ok && rg.lir == 0) {
+        // bias on the projection output, then the combine, then the router
+        // weight (pulsar_kernels.cu:2606-2612)
+        if (p.gate_b) g += p.gate_b[row];
+        if (p.up_b) u += p.up_b[row];
+        mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
+    }
+}
+
+template <uint32_t Q, uint32_t UPLMAX>
+__global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
+                                                       const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                       const pulsar_block_q8_K *__restrict__ midq,
+                                                       uint32_t n_units, uint32_t nblk32,
+                                                       uint32_t lpr_log2, uint32_t mid_blocks,
+                                                       uint32_t out_dim, uint32_t n_used,
+                                                       uint64_t row_bytes) {
+    PK_IQ2_LUT(Q)
+    __shared__ float part[kSlotChunk][16];
+    const uint32_t token = blockIdx.y;
+    const uint32_t wave = threadIdx.x / 64u;
+    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> lpr_log2;
+    const uint32_t row = blockIdx.x * rpp + rg.rip;
+    const bool row_ok = row < out_dim;
+    float total = 0.0f;
+    for (uint32_t base = 0; base < n_used; base += kSlotChunk) {
+        const uint32_t end = base + kSlotChunk < n_used ? base + kSlotChunk : n_used;
+        for (uint32_t s = base + wave; s < end; s += kWaves) {
+            const uint64_t so = (uint64_t)token * n_used + s;
+            const pulsar_expert_ptrs p = ptrs[so];
+            // -0.0 is the additive identity for every float, so a skipped
+            // slot (NULL down, pulsar_kernels.cu:2635) leaves the sum as is
+            float v = -0.0f;
+            if (p.down) {
+                Act a[UPLMAX];
+                load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
+                typename Fmt<Q>::W w[UPLMAX];
+                load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)row * row_bytes, row_ok, rg, w);
+                v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
+            }
+            if (rg.lir == 0) part[s - base][rg.rip] = v;
+        }
+        __syncthreads();
+        if (wave == 0 && rg.lir == 0)
+            for (uint32_t s = base; s < end; s++) total += part[s - base][rg.rip];
+        __syncthreads();
+    }
+    if (wave == 0 && rg.lir == 0 && row_ok) out[(uint64_t)token * out_dim + row] = total;
+}
+
+template <uint32_t Q, uint32_t UPLMAX>
+__global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
+        float *__restrict__ mid, const pulsar_expert_ptrs *__restrict__ gptrs,
+        const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
+        const float *__restrict__ weights, const pulsar_block_q8_K *__restrict__ xq,
+        uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t mid_dim,
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op) {
+    PK_IQ2_LUT(Q)
+    const uint32_t group = blockIdx.y;
+    const pulsar_expert_ptrs p = gptrs[group];
+    if (!p.gate || !p.up) return;
+    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> lpr_log2;
+    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
+    const bool row_ok = row < mid_dim;
+    typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)row * row_bytes, row_ok, rg, wg);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)row * row_bytes, row_ok, rg, wu);
+    const float gb = row_ok && p.gate_b ? p.gate_b[row] : 0.0f;
+    const float ub = row_ok && p.up_b ? p.up_b[row] : 0.0f;
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    for (uint32_t i = s0; i < s1; i++) {
+        const uint32_t pr = pairs[i];
+        const uint32_t token = pr >> 4, slot = pr & 15u;
+        const uint64_t so = (uint64_t)token * n_used + slot;
+        Act a[UPLMAX];
+        load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
+        float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
+        float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
+        if (row_ok && rg.lir == 0) {
+            if (p.gate_b) g += gb;
+            if (p.up_b) u += ub;
+            mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
+        }
+    }
+}
+
+template <uint32_t Q, uint32_t UPLMAX>
+__global__ __launch_bounds__(256) void moe_down_grouped_kernel(
+        float *__restrict__ partial, const pulsar_expert_ptrs *__restrict__ gptrs,
+        const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
+        const pulsar_block_q8_K *__restrict__ midq, uint32_t n_units, uint32_t nblk32,
+        uint32_t lpr_log2, uint32_t mid_blocks, uint32_t out_dim, uint32_t n_used,
+        uint64_t row_bytes) {
+    PK_IQ2_LUT(Q)
+    const uint32_t group = blockIdx.y;
+    const pulsar_expert_ptrs p = gptrs[group];
+    if (!p.down) return;
+    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> lpr_log2;
+    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
+    const bool row_ok = row < out_dim;
+    typename Fmt<Q>::W w[UPLMAX];
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)row * row_bytes, row_ok, rg, w);
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    for (uint32_t i = s0; i < s1; i++) {
+        const uint32_t pr = pairs[i];
+        const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+        Act a[UPLMAX];
+        load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
+        const float v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
+        if (row_ok && rg.lir == 0) partial[so * out_dim + row] = v;
+    }
+}
+
+// Deterministic slot reduce (pulsar_kernels.cu:2791-2806).
+__global__ __launch_bounds__(256) void slot_sum_kernel(float *__restrict__ out,
+                                                       const float *__restrict__ partial,
+                                                       uint32_t out_dim, uint32_t n_used,
+                                                       uint64_t total) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const uint64_t token = gid / out_dim;
+    const uint64_t row = gid - token * out_dim;
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < n_used; s++) acc += partial[(token * n_used + s) * out_dim + row];
+    out[gid] = acc;
+}
+
+// out += sum_s w_s * down_b_s (pulsar_kernels.cu:3601-3619).
+__global__ __launch_bounds__(256) void down_bias_kernel(float *__restrict__ out,
+                                                        const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                        const float *__restrict__ weights,
+                                                        uint32_t out_dim, uint32_t n_used,
+                                                        uint64_t total) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const uint64_t token = gid / out_dim;
+    const uint64_t row = gid - token * out_dim;
+    float b = 0.0f;
+    for (uint32_t s = 0; s < n_used; s++) {
+        const uint64_t so = token * n_used + s;
+        const float *db = ptrs[so].down_b;
+        if (db) b += weights[so] * db[row];
+    }
+    if (b != 0.0f) out[gid] += b;
+}
+
+// ------------------------------------------------------------ dispatch --
+
+struct Geo {
+    uint32_t n_units, nblk32, l2, upl, blocks;
+};
+
+static Geo geo_for(uint32_t quant, uint32_t k_dim) {
+    Geo g;
+    g.n_units = units_per_row(quant, k_dim);
+    g.nblk32 = (k_dim + 31u) / 32u;
+    g.l2 = lpr_log2_for(g.n_units);
+    g.upl = (g.n_units + (1u << g.l2) - 1u) >> g.l2;
+    g.blocks = (k_dim + 255u) / 256u;
+    return g;
+}
+
+static bool quant_ok(uint32_t q) {
+    return q == PULSAR_QUANT_Q2_K || q == PULSAR_QUANT_IQ2_XXS || q == PULSAR_QUANT_Q4_K ||
+           q == PULSAR_QUANT_Q6_K || q == PULSAR_QUANT_MXFP4;
+}
+
+// Calls F::template run<Q, UPLMAX>() for the run-time (quant, upl);
+// MAXU bounds the instantiated unit counts (the grouped kernels hold two
+// weight rows in registers and would spill beyond 4 units per lane).
+template <uint32_t MAXU, typename F>
+static int with_format(uint32_t quant, uint32_t upl, F &&f) {
+#define PK_UPL(Q)                                                   \
+    if (upl <= 1u) return f.template run<Q, 1>();                   \
+    if (upl <= 2u) return f.template run<Q, 2>();                   \
+    if (upl <= 4u) return f.template run<Q, 4>();                   \
+    if (MAXU >= 8u && upl <= 8u) return f.template run<Q, (MAXU >= 8u ? 8u : 4u)>(); \
+    return reject("moe (row width above the supported maximum)");
+    switch (quant) {
+    case PULSAR_QUANT_Q2_K: PK_UPL(PULSAR_QUANT_Q2_K)
+    case PULSAR_QUANT_IQ2_XXS: PK_UPL(PULSAR_QUANT_IQ2_XXS)
+    case PULSAR_QUANT_Q4_K: PK_UPL(PULSAR_QUANT_Q4_K)
+    case PULSAR_QUANT_Q6_K: PK_UPL(PULSAR_QUANT_Q6_K)
+    case PULSAR_QUANT_MXFP4: PK_UPL(PULSAR_QUANT_MXFP4)
+    default: return reject("moe (quant)");
+    }
+#undef PK_UPL
+}
+
+struct PairLaunch {
+    void *mid;
+    const void *ptrs, *weights, *xq;
+    uint32_t mid_dim, n_used, n_tok, act_op;
+    uint64_t row_bytes;
+    Geo g;
+    template <uint32_t Q, uint32_t U>
+    int run() {
+        const uint32_t rpb = kWaves * (64u >> g.l2);
+        const dim3 grid((mid_dim + rpb - 1u) / rpb, n_used, n_tok);
+        hipLaunchKernelGGL((moe_pair_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)mid,
+                           (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
+                           (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
+                           mid_dim, n_used, row_bytes, act_op);
+        return launch_ok("moe pair swiglu launch");
+    }
+};
+
+struct DownLaunch {
+    void *out;
+    const void *ptrs, *midq;
+    uint32_t out_dim, n_used, n_tok;
+    uint64_t row_bytes;
+    Geo g;
+    template <uint32_t Q, uint32_t U>
+    int run() {
+        const uint32_t rpp = 64u >> g.l2;
+        const dim3 grid((out_dim + rpp - 1u) / rpp, n_tok);
+        hipLaunchKernelGGL((moe_down_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)out,
+                           (const pulsar_expert_ptrs *)ptrs, (const pulsar_block_q8_K *)midq,
+                           g.n_units, g.nblk32, g.l2, g.blocks, out_dim, n_used, row_bytes);
+        return launch_ok("moe down launch");
+    }
+};
+
+struct PairGroupedLaunch {
+    void *mid;
+    const void *gptrs, *starts, *pairs, *weights, *xq;
+    uint32_t mid_dim, n_used, n_group, act_op;
+    uint64_t row_bytes;
+    Geo g;
+    template <uint32_t Q, uint32_t U>
+    int run() {
+        const uint32_t rpb = kWaves * (64u >> g.l2);
+        const dim3 grid((mid_dim + rpb - 1u) / rpb, n_group);
+        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)mid,
+                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts,
+                           (const uint32_t *)pairs, (const float *)weights,
+                           (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
+                           mid_dim, n_used, row_bytes, act_op);
+        return launch_ok("moe pair swiglu grouped launch");
+    }
+};
+
+struct DownGroupedLaunch {
+    void *partial;
+    const void *gptrs, *starts, *pairs, *midq;
+    uint32_t out_dim, n_used, n_group;
+    uint64_t row_bytes;
+    Geo g;
+    template <uint32_t Q, uint32_t U>
+    int run() {
+        const uint32_t rpb = kWaves * (64u >> g.l2);
+        const dim3 grid((out_dim + rpb - 1u) / rpb, n_group);
+        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), 0, 0,
+                           (float *)partial, (const pulsar_expert_ptrs *)gptrs,
+                           (const uint32_t *)starts, (const uint32_t *)pairs,
+                           (const pulsar_block_q8_K *)midq, g.n_units, g.nblk32, g.l2, g.blocks,
+                           out_dim, n_used, row_bytes);
+        return launch_ok("moe down grouped launch");
+    }
+};
+
+}  // namespace pk
+
+using namespace pk;
+
+extern "C" int pulsar_moe_pair_swiglu(void *mid, const void *ptrs, const void *weights,
+                                      const void *xq, uint32_t in_dim, uint32_t mid_dim,
+                                      uint32_t n_used, uint32_t n_tok, uint64_t row_bytes,
+                                      uint32_t quant, uint32_t act_op) {
+    if (!mid || !ptrs || !weights || !xq || in_dim == 0 || mid_dim == 0 || n_used == 0 ||
+        n_tok == 0 || row_bytes == 0 || (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI) ||
+        n_used > 65535u || n_tok > 65535u)
+        return reject("moe pair swiglu");
+    const Geo g = geo_for(quant, in_dim);
+    PairLaunch f{mid, ptrs, weights, xq, mid_dim, n_used, n_tok, act_op, row_bytes, g};
+    if (!quant_ok(quant)) return reject("moe pair swiglu (quant)");
+    return with_format<8>(quant, g.upl, f);
+}
+
+extern "C" int pulsar_moe_down(void *out, const void *ptrs, const void *midq, uint32_t mid_dim,
+                               uint32_t out_dim, uint32_t n_used, uint32_t n_tok, uint64_t row_bytes,
+                               uint32_t quant) {
+    if (!out || !ptrs || !midq || mid_dim == 0 || out_dim == 0 || n_used == 0 || n_tok == 0 ||
+        row_bytes == 0 || n_tok > 65535u)
+        return reject("moe down");
+    const Geo g = geo_for(quant, mid_dim);
+    DownLaunch f{out, ptrs, midq, out_dim, n_used, n_tok, row_bytes, g};
+    if (!quant_ok(quant)) return reject("moe down (quant)");
+    return with_format<8>(quant, g.upl, f);
+}
+
+// Grouped entry points keep the reference's argument contract
+// (pulsar_kernels.cu:3488-3492, 3541-3547): in_dim (pair) and mid_dim (down)
+// multiples of 256, n_used <= 16 (4-bit slot field in `pairs`).
+extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *starts,
+                                              const void *pairs, const void *weights,
+                                              const void *xq, uint32_t in_dim, uint32_t mid_dim,
+                                              uint32_t n_used, uint32_t n_group,
+                                              uint64_t row_bytes, uint32_t quant,
+                                              uint32_t act_op) {
+    if (!mid || !gptrs || !starts || !pairs || !weights || !xq || in_dim == 0 ||
+        in_dim % 256u != 0 || mid_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 ||
+        n_group > 65535u || row_bytes == 0 ||
+        (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI))
+        return reject("moe pair swiglu grouped");
+    const Geo g = geo_for(quant, in_dim);
+    PairGroupedLaunch f{mid, gptrs, starts, pairs, weights, xq, mid_dim, n_used, n_group, act_op, row_bytes, g};
+    if (!quant_ok(quant)) return reject("moe pair swiglu grouped (quant)");
+    return with_format<4>(quant, g.upl, f);
+}
+
+extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const void *starts,
+                                       const void *pairs, const void *midq, uint32_t mid_dim,
+                                       uint32_t out_dim, uint32_t n_used, uint32_t n_group,
+                                       uint64_t row_bytes, uint32_t quant) {
+    if (!partial || !gptrs || !starts || !pairs || !midq || mid_dim == 0 || mid_dim % 256u != 0 ||
+        out_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 || n_group > 65535u ||
+        row_bytes == 0)
+        return reject("moe down grouped");
+    const Geo g = geo_for(quant, mid_dim);
+    DownGroupedLaunch f{partial, gptrs, starts, pairs, midq, out_dim, n_used, n_group, row_bytes, g};
+    if (!quant_ok(quant)) return reject("moe down grouped (quant)");
+    return with_format<4>(quant, g.upl, f);
+}
+
+extern "C" int pulsar_moe_slot_sum(void *out, const void *partial, uint32_t out_dim, uint32_t n_used,
+                                   uint32_t n_tok) {
+    if (!out || !partial || out_dim == 0 || n_used == 0 || n_tok == 0) return reject("moe slot sum");
+    const uint64_t total = (uint64_t)n_tok * out_dim;
+    hipLaunchKernelGGL(slot_sum_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, 0,
+                       (float *)out, (const float *)partial, out_dim, n_used, total);
+    return launch_ok("moe slot sum launch");
+}
+
+extern "C" int pulsar_moe_down_bias(void *out, const void *ptrs, const void *weights,
+                                    uint32_t out_dim, uint32_t n_used, uint32_t n_tok) {
+    if (!out || !ptrs || !weights || out_dim == 0 || n_used == 0 || n_tok == 0)
+        return reject("moe down bias");
+    const uint64_t total = (uint64_t)n_tok * out_dim;
+    hipLaunchKernelGGL(down_bias_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, 0,
+                       (float *)out, (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
+                       out_dim, n_used, total);
+    return launch_ok("moe down bias launch");
+}

@@ -1,0 +1,126 @@
+// pk_common.h - device helpers shared by every kernel of libpulsar_moe.
+//
+// Target: gfx950 (CDNA4), wave64. Compiled with -ffp-contract=off so every
+// fp32 expression rounds in source order, like the reference's CPU lane
+// (crates/quant/src/cpu_dot.rs never fuses a*b+c).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/pulsar_moe.h"
+
+#define PK_DEV __device__ __forceinline__
+
+namespace pk {
+
+constexpr uint32_t kWave = 64;
+
+// Error reporting with the reference's message shape (pulsar_kernels.cu:25-29).
+static inline int launch_ok(const char *what) {
+    const hipError_t err = hipGetLastError();
+    if (err == hipSuccess) return 1;
+    fprintf(stderr, "pulsar-kernels: %s: %s\n", what, hipGetErrorString(err));
+    return 0;
+}
+
+static inline int reject(const char *what) {
+    fprintf(stderr, "pulsar-kernels: %s: invalid arguments\n", what);
+    return 0;
+}
+
+// ---------------------------------------------------------------- loads --
+// Weight blocks sit at 1/2/4-byte alignment inside rows (MXFP4 17 B,
+// Q6_K 210 B, IQ2_XXS 66 B, Q2_K 84 B); gfx950 global loads accept any
+// byte alignment, so these compile to single global_load_dword[x2|x4].
+PK_DEV uint32_t ld32(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+PK_DEV uint2 ld64(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+PK_DEV uint4 ld128(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+PK_DEV uint16_t ld16(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+// Exact f16 -> f32 (v_cvt_f32_f16 is exact for every finite f16).
+PK_DEV float f16f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Signed 4 x int8 dot product accumulated into int32 (v_dot4_i32_i8).
+PK_DEV int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// --------------------------------------------------------- cross-lane ----
+// Partner value for the reduction step that doubles the group size from s
+// to 2s lanes (aligned groups). Steps 1 and 2 are quad permutes, 4 and 8
+// mirror the half-row / row (lane i <-> 7-i / 15-i: the partner lies in the
+// other half of the 2s group, which is all a sum needs), 16 is a ds_swizzle
+// xor and 32 a cross-half bpermute.
+PK_DEV int32_t partner(int32_t v, uint32_t s) {
+    switch (s) {
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    case 4: return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    case 8: return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+    case 16: return __builtin_amdgcn_ds_swizzle(v, 0x401F);                    // xor 16
+    default: return __shfl_xor(v, 32, 64);                                     // xor 32
+    }
+}
+PK_DEV float partner(float v, uint32_t s) {
+    return __builtin_bit_cast(float, partner(__builtin_bit_cast(int32_t, v), s));
+}
+
+// Sum over aligned groups of G lanes (G a power of two <= 64); every lane
+// of the group ends with the group total. Integer sums are exact in any
+// order; float sums follow this fixed tree.
+template <uint32_t G, typename T>
+PK_DEV T group_sum(T v) {
+#pragma unroll
+    for (uint32_t s = 1; s < G; s <<= 1) v += partner(v, s);
+    return v;
+}
+
+// Same with a run-time group size (uniform across the wave), starting after
+// the groups of `from` lanes have already been summed.
+template <typename T>
+PK_DEV T group_sum_from(T v, uint32_t from, uint32_t g) {
+    for (uint32_t s = from; s < g; s <<= 1) v += partner(v, s);
+    return v;
+}
+
+PK_DEV int32_t lane_xor(int32_t v, uint32_t m) { return __shfl_xor(v, (int)m, 64); }
+PK_DEV float lane_xor(float v, uint32_t m) { return __shfl_xor(v, (int)m, 64); }
+
+PK_DEV float wave_max(float v) {
+#pragma unroll
+    for (uint32_t m = 1; m < 64; m <<= 1) v = fmaxf(v, lane_xor(v, m));
+    return v;
+}
+
+// ------------------------------------------------------------ combine --
+// Gated combine (pulsar_kernels.cu:124-141 == crates/engine/src/lib.rs:2131-2157):
+// op 0 silu(g) * u; op 2 swiglu_oai (gate clamped above at 7, up to +-7,
+// sigmoid sharpened by 1.702, up + 1). expf is the device libm's.
+PK_DEV float glu(float g, float u, uint32_t op) {
+    if (op == 2u) {
+        g = fminf(g, 7.0f);
+        u = fminf(fmaxf(u, -7.0f), 7.0f);
+        return g / (1.0f + expf(-1.702f * g)) * (u + 1.0f);
+    }
+    return g / (1.0f + expf(-g)) * u;
+}
+
+}  // namespace pk

@@ -1,0 +1,137 @@
+"""Host-side mirror of the reference's kernel wrappers (crates/kernels/src/lib.rs).
+
+Each function has the reference wrapper's name and argument order, takes
+device buffers (torch CUDA tensors or raw device addresses as ints) and raises
+KernelError(op) where the Rust wrapper returns Err(Error(op)) (the C entry
+point returned 0; crates/kernels/src/lib.rs:212-218). Launches are
+asynchronous on the null stream; call torch.cuda.synchronize() (the
+reference's kernels::sync) before reading results on the host.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import _lib
+from .formats import EXPERT_PTRS_BYTES
+
+
+class KernelError(RuntimeError):
+    """A kernel entry point returned 0 (crates/kernels/src/lib.rs:8-20)."""
+
+    def __init__(self, op: str):
+        super().__init__(f"hip kernel op failed: {op}")
+        self.op = op
+
+
+def _ptr(buf) -> int:
+    if buf is None:
+        return 0
+    if isinstance(buf, int):
+        return buf
+    if hasattr(buf, "data_ptr"):
+        if not buf.is_cuda:
+            raise ValueError("device buffer expected (got a host tensor)")
+        return buf.data_ptr()
+    raise TypeError(f"cannot take a device address of {type(buf)!r}")
+
+
+def _check(ret: int, op: str) -> None:
+    if ret == 0:
+        raise KernelError(op)
+
+
+def quantize_q8_k(out, x, in_dim: int, n_rows: int) -> None:
+    _check(_lib.load().pulsar_quantize_q8_K(_ptr(out), _ptr(x), in_dim, n_rows), "quantize_q8_k")
+
+
+def matmul_kq(out, w, xq, in_dim: int, out_dim: int, n_tok: int, row_bytes: int, quant: int) -> None:
+    _check(
+        _lib.load().pulsar_matmul_kq(_ptr(out), _ptr(w), _ptr(xq), in_dim, out_dim, n_tok, row_bytes, quant),
+        "matmul_kq",
+    )
+
+
+def moe_pair_swiglu(mid, ptrs, weights, x, in_dim: int, mid_dim: int, n_used: int, n_tok: int,
+                    row_bytes: int, quant: int, act_op: int) -> None:
+    _check(
+        _lib.load().pulsar_moe_pair_swiglu(_ptr(mid), _ptr(ptrs), _ptr(weights), _ptr(x), in_dim, mid_dim,
+                                           n_used, n_tok, row_bytes, quant, act_op),
+        "moe_pair_swiglu",
+    )
+
+
+def moe_down(out, ptrs, mid, mid_dim: int, out_dim: int, n_used: int, n_tok: int, row_bytes: int,
+             quant: int) -> None:
+    _check(
+        _lib.load().pulsar_moe_down(_ptr(out), _ptr(ptrs), _ptr(mid), mid_dim, out_dim, n_used, n_tok,
+                                    row_bytes, quant),
+        "moe_down",
+    )
+
+
+def moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, weights, xq, in_dim: int, mid_dim: int,
+                            n_used: int, n_group: int, row_bytes: int, quant: int, act_op: int) -> None:
+    _check(
+        _lib.load().pulsar_moe_pair_swiglu_grouped(_ptr(mid), _ptr(gptrs), _ptr(starts), _ptr(pairs),
+                                                   _ptr(weights), _ptr(xq), in_dim, mid_dim, n_used,
+                                                   n_group, row_bytes, quant, act_op),
+        "moe_pair_swiglu_grouped",
+    )
+
+
+def moe_down_grouped(partial, gptrs, starts, pairs, midq, mid_dim: int, out_dim: int, n_used: int,
+                     n_group: int, row_bytes: int, quant: int) -> None:
+    _check(
+        _lib.load().pulsar_moe_down_grouped(_ptr(partial), _ptr(gptrs), _ptr(starts), _ptr(pairs),
+                                            _ptr(midq), mid_dim, out_dim, n_used, n_group, row_bytes,
+                                            quant),
+        "moe_down_grouped",
+    )
+
+
+def moe_slot_sum(out, partial, out_dim: int, n_used: int, n_tok: int) -> None:
+    _check(_lib.load().pulsar_moe_slot_sum(_ptr(out), _ptr(partial), out_dim, n_used, n_tok), "moe_slot_sum")
+
+
+def moe_down_bias(out, ptrs, weights, out_dim: int, n_used: int, n_tok: int) -> None:
+    _check(
+        _lib.load().pulsar_moe_down_bias(_ptr(out), _ptr(ptrs), _ptr(weights), out_dim, n_used, n_tok),
+        "moe_down_bias",
+    )
+
+
+def add_bias_rows(x, bias, dim: int, rows: int) -> None:
+    _check(_lib.load().pulsar_add_bias_rows(_ptr(x), _ptr(bias), dim, rows), "add_bias_rows")
+
+
+def router_select(selected, weights, logits, bias, n_expert: int, k_used: int, weight_scale: float,
+                  n_tok: int, mode: int, n_shexp: int) -> None:
+    _check(
+        _lib.load().pulsar_router_select(_ptr(selected), _ptr(weights), _ptr(logits), _ptr(bias), n_expert,
+                                         k_used, weight_scale, n_tok, mode, n_shexp),
+        "router_select",
+    )
+
+
+def matmul_f32(out, w, x, in_dim: int, out_dim: int, n_tok: int) -> None:
+    _check(_lib.load().pulsar_matmul_f32(_ptr(out), _ptr(w), _ptr(x), in_dim, out_dim, n_tok), "matmul_f32")
+
+
+def bw_read(buf, nbytes: int, sink) -> None:
+    _check(_lib.load().pulsar_bw_read(_ptr(buf), nbytes, _ptr(sink)), "bw_read")
+
+
+EXPERT_PTRS_DTYPE = np.dtype(
+    [("gate", "<u8"), ("up", "<u8"), ("down", "<u8"), ("gate_b", "<u8"), ("up_b", "<u8"), ("down_b", "<u8")]
+)
+assert EXPERT_PTRS_DTYPE.itemsize == EXPERT_PTRS_BYTES
+
+
+def expert_ptrs(entries) -> np.ndarray:
+    """Packs (gate, up, down[, gate_b, up_b, down_b]) address tuples (0 = NULL)
+    into the 48-byte pulsar_expert_ptrs layout (crates/kernels/src/lib.rs:21-49)."""
+    arr = np.zeros(len(entries), dtype=EXPERT_PTRS_DTYPE)
+    for i, e in enumerate(entries):
+        e = tuple(e) + (0,) * (6 - len(e))
+        arr[i] = tuple(int(v) for v in e)
+    return arr

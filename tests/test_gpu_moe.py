@@ -1,0 +1,226 @@
+"""GPU parity of the routed-MoE stages against the oracle.
+
+Stage tolerances (derived from the row-dot tolerance in tests/gpu_util.py):
+  pair : |d mid| <= 1e-5 * w * (1.5 (|u|+1) A_g + (|g|+1) A_u) + 4e-7 |mid|,
+         A_g, A_u = sum_b |f_b| of the gate/up row dots; the last term covers
+         the device expf against the host expf (a few ulp);
+  down : fed the oracle's own mid q8_K, |d out| <= 1e-5 * sum_s A_s;
+  slot sum, down bias: bit-exact (same operation order on both sides).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pulsar_amd import kernels as K
+from pulsar_amd import synth
+from pulsar_amd.formats import (ACT_SILU, ACT_SWIGLU_OAI, QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K,
+                                QUANT_Q6_K, row_bytes)
+from tests.gpu_util import TOL_REL, down, up, up_f32, zeros_f32
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(2024)
+
+
+class Layer:
+    """A small expert bank on host and device, with routed (token, slot) pointers."""
+
+    def __init__(self, gq, dq, hidden, ffn, E, n_used, n_tok, biases=False, null_slots=(), seed=0):
+        self.gq, self.dq, self.hidden, self.ffn, self.E = gq, dq, hidden, ffn, E
+        self.n_used, self.n_tok = n_used, n_tok
+        self.grb, self.drb = row_bytes(gq, hidden), row_bytes(dq, ffn)
+        r = synth.rng_for(seed, f"layer{gq}{dq}{hidden}{ffn}")
+        self.g = synth.quant_matrix(gq, E * ffn, hidden, r).reshape(E, ffn, -1)
+        self.u = synth.quant_matrix(gq, E * ffn, hidden, r).reshape(E, ffn, -1)
+        self.d = synth.quant_matrix(dq, E * hidden, ffn, r).reshape(E, hidden, -1)
+        self.gb = self.ub = self.db = None
+        if biases:
+            self.gb = (r.standard_normal((E, ffn)) * 0.02).astype(np.float32)
+            self.ub = (r.standard_normal((E, ffn)) * 0.02).astype(np.float32)
+            self.db = (r.standard_normal((E, hidden)) * 0.02).astype(np.float32)
+        self.sel = r.integers(0, E, (n_tok, n_used))
+        for si in null_slots:
+            self.sel.reshape(-1)[si] = -1
+        self.w = r.uniform(0.1, 1.0, (n_tok, n_used)).astype(np.float32)
+        self.x = r.standard_normal((n_tok, hidden)).astype(np.float32)
+        # device copies (+256 B slack after each bank, like the engine's slabs)
+        self.dg, self.du, self.dd = (up(np.concatenate([a.reshape(-1), np.zeros(256, np.uint8)]))
+                                     for a in (self.g, self.u, self.d))
+        self.dbias = [None if b is None else up_f32(b) for b in (self.gb, self.ub, self.db)]
+
+    def host_entries(self, e):
+        if e < 0:
+            return (None,) * 6
+        b = [None if a is None else a[e] for a in (self.gb, self.ub, self.db)]
+        return (self.g[e], self.u[e], self.d[e], *b)
+
+    def dev_entries(self, e):
+        if e < 0:
+            return (0,) * 6
+        gb, ub, db = self.dbias
+        return (self.dg.data_ptr() + e * self.ffn * self.grb, self.du.data_ptr() + e * self.ffn * self.grb,
+                self.dd.data_ptr() + e * self.hidden * self.drb,
+                0 if gb is None else gb.data_ptr() + e * self.ffn * 4,
+                0 if ub is None else ub.data_ptr() + e * self.ffn * 4,
+                0 if db is None else db.data_ptr() + e * self.hidden * 4)
+
+    def ptrs(self):
+        flat = self.sel.reshape(-1)
+        return (oracle.host_ptrs([self.host_entries(e) for e in flat]),
+                up(K.expert_ptrs([self.dev_entries(e) for e in flat])))
+
+
+def pair_bound(L: Layer, xq, act_op):
+    """Per (token*slot, row) tolerance for the pair stage."""
+    bound = np.zeros((L.n_tok * L.n_used, L.ffn))
+    for t in range(L.n_tok):
+        for s in range(L.n_used):
+            e = L.sel[t, s]
+            if e < 0:
+                continue
+            for r in range(L.ffn):
+                g, ag = oracle.vec_dot(L.gq, L.g[e, r], xq[t], L.hidden)
+                u, au = oracle.vec_dot(L.gq, L.u[e, r], xq[t], L.hidden)
+                bound[t * L.n_used + s, r] = TOL_REL * L.w[t, s] * (1.5 * (abs(u) + 1) * ag + (abs(g) + 1) * au)
+    return bound
+
+
+def down_bound(L: Layer, midq):
+    mb = -(-L.ffn // 256) * 292
+    bound = np.zeros((L.n_tok, L.hidden))
+    for t in range(L.n_tok):
+        for s in range(L.n_used):
+            e = L.sel[t, s]
+            if e < 0:
+                continue
+            q = midq[t * L.n_used + s]
+            for r in range(L.hidden):
+                bound[t, r] += oracle.vec_dot(L.dq, L.d[e, r], q, L.ffn)[1]
+    return TOL_REL * bound + 1e-30
+
+
+def run_pair(L: Layer, act_op, dptrs, xq):
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu(mid, dptrs, up_f32(L.w), up(xq), L.hidden, L.ffn, L.n_used, L.n_tok, L.grb, L.gq, act_op)
+    return down(mid)
+
+
+def check_pair_down(L: Layer, act_op):
+    hptrs, dptrs = L.ptrs()
+    xq = oracle.quantize_q8_k(L.x)
+    got_mid = run_pair(L, act_op, dptrs, xq)
+    want_mid = oracle.moe_pair_swiglu(hptrs, L.w, xq, L.hidden, L.ffn, L.n_used, L.n_tok, L.grb, L.gq, act_op)
+    bound = pair_bound(L, xq, act_op) + 4e-7 * np.abs(want_mid) + 1e-30
+    err = np.abs(got_mid.astype(np.float64) - want_mid)
+    assert (err <= bound).all(), f"pair: max err {err.max():.3e} (worst ratio {(err / bound).max():.2f})"
+    for si, e in enumerate(L.sel.reshape(-1)):
+        if e < 0:
+            assert not got_mid[si].any()  # NULL slot writes zeros
+    # down on the oracle's own mid q8_K
+    midq = oracle.quantize_q8_k(want_mid)
+    out = zeros_f32((L.n_tok, L.hidden))
+    K.moe_down(out, dptrs, up(midq), L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, L.dq)
+    got = down(out)
+    want = oracle.moe_down(hptrs, midq, L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, L.dq)
+    err = np.abs(got.astype(np.float64) - want)
+    bound = down_bound(L, midq)
+    assert (err <= bound).all(), f"down: max err {err.max():.3e} (worst ratio {(err / bound).max():.2f})"
+    return hptrs, dptrs, xq, want_mid, midq, want
+
+
+@pytest.mark.parametrize("gq,dq", [(QUANT_Q4_K, QUANT_Q6_K), (QUANT_Q2_K, QUANT_Q2_K),
+                                   (QUANT_IQ2_XXS, QUANT_IQ2_XXS), (QUANT_Q6_K, QUANT_Q4_K)])
+def test_pair_down_kquants(dev, gq, dq):
+    L = Layer(gq, dq, hidden=512, ffn=256, E=8, n_used=4, n_tok=3, null_slots=(6,))
+    check_pair_down(L, ACT_SILU)
+
+
+@pytest.mark.parametrize("hidden,ffn", [(2880, 704), (512, 320)])
+def test_pair_down_mxfp4_tails_biases_oai(dev, hidden, ffn):
+    L = Layer(QUANT_MXFP4, QUANT_MXFP4, hidden=hidden, ffn=ffn, E=4, n_used=4, n_tok=2, biases=True,
+              null_slots=(1,))
+    hptrs, dptrs, xq, mid, midq, out = check_pair_down(L, ACT_SWIGLU_OAI)
+    # down bias: bit-exact against the oracle
+    d_out = up_f32(out)
+    K.moe_down_bias(d_out, dptrs, up_f32(L.w), L.hidden, L.n_used, L.n_tok)
+    want = oracle.moe_down_bias(out, hptrs, L.w, L.hidden, L.n_used, L.n_tok)
+    assert np.array_equal(down(d_out), want)
+
+
+def test_pair_down_decode_shapes(dev):
+    """The c3 shape (hidden 2048, FFN 512, 8 routed + 1 shared slot) at a
+    reduced expert count."""
+    L = Layer(QUANT_Q4_K, QUANT_Q6_K, hidden=2048, ffn=512, E=10, n_used=9, n_tok=1)
+    check_pair_down(L, ACT_SILU)
+
+
+@pytest.mark.parametrize("gq", [QUANT_Q2_K, QUANT_IQ2_XXS])
+def test_grouped_matches_plain_and_oracle(dev, gq):
+    L = Layer(gq, gq, hidden=1024, ffn=512, E=6, n_used=4, n_tok=16, null_slots=(3, 17))
+    hptrs, dptrs, xq, want_mid, midq, want_out = check_pair_down(L, ACT_SILU)
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu_grouped(mid, gptrs, up(starts), up(pairs), up_f32(L.w), up(xq), L.hidden, L.ffn,
+                              L.n_used, len(ids), L.grb, gq, ACT_SILU)
+    plain = run_pair(L, ACT_SILU, dptrs, xq)
+    assert np.array_equal(down(mid), plain)  # same kernels' math, same order
+    partial = zeros_f32((L.n_tok * L.n_used, L.hidden))
+    K.moe_down_grouped(partial, gptrs, up(starts), up(pairs), up(midq), L.ffn, L.hidden, L.n_used, len(ids),
+                       L.drb, gq)
+    out = zeros_f32((L.n_tok, L.hidden))
+    K.moe_slot_sum(out, partial, L.hidden, L.n_used, L.n_tok)
+    err = np.abs(down(out).astype(np.float64) - want_out)
+    bound = down_bound(L, midq)
+    assert (err <= bound).all(), f"grouped down: max err {err.max():.3e}"
+    # slot sum is the in-order sum of the partials
+    p = down(partial).reshape(L.n_tok, L.n_used, L.hidden)
+    acc = np.zeros((L.n_tok, L.hidden), np.float32)
+    for s in range(L.n_used):
+        acc += p[:, s]
+    assert np.array_equal(down(out), acc)
+
+
+def test_grouped_contract(dev):
+    buf = up(np.zeros(4096, np.uint8))
+    with pytest.raises(K.KernelError):  # in_dim % 256 (pulsar_kernels.cu:3488)
+        K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 2880, 64, 4, 1, 1530, QUANT_MXFP4, 0)
+    with pytest.raises(K.KernelError):  # n_used > 16 cannot be packed in pairs
+        K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 256, 64, 17, 1, 144, QUANT_Q4_K, 0)
+    with pytest.raises(K.KernelError):  # mid_dim % 256 for the grouped down
+        K.moe_down_grouped(buf, buf, buf, buf, buf, 704, 64, 4, 1, 374, QUANT_MXFP4)
+    with pytest.raises(K.KernelError):
+        K.moe_pair_swiglu(buf, buf, buf, buf, 256, 64, 4, 1, 144, 99, 0)  # unknown quant
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ router --
+
+@pytest.mark.parametrize("n_expert,k,n_tok,mode", [(256, 8, 1, 1), (128, 8, 16, 1), (32, 4, 64, 1),
+                                                   (64, 8, 7, 0), (896, 16, 3, 1), (256, 6, 5, 2)])
+def test_router_select(dev, n_expert, k, n_tok, mode):
+    n_sh = 2 if mode == 2 else 0
+    logits = (rng.standard_normal((n_tok, n_expert + n_sh)) * 4).astype(np.float32)
+    bias = rng.standard_normal(n_expert).astype(np.float32) if mode != 1 else np.zeros(n_expert, np.float32)
+    n_slot = k + n_sh
+    sel = torch.zeros((n_tok, n_slot), dtype=torch.int32, device=dev)
+    w = zeros_f32((n_tok, n_slot))
+    K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.5, n_tok, mode, n_sh)
+    want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.5, n_tok, mode, n_sh)
+    assert np.array_equal(down(sel), want_sel)
+    assert np.allclose(down(w), want_w, rtol=0, atol=1e-6)
+
+
+def test_matmul_f32_and_bias(dev):
+    for in_dim, out_dim, n_tok in ((2048, 256, 1), (4096, 128, 16), (2880, 32, 64), (37, 5, 3)):
+        wt = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float32)
+        x = rng.standard_normal((n_tok, in_dim)).astype(np.float32)
+        out = zeros_f32((n_tok, out_dim))
+        K.matmul_f32(out, up_f32(wt), up_f32(x), in_dim, out_dim, n_tok)
+        want = oracle.matmul_f32(wt, x, in_dim, out_dim, n_tok)
+        scale = np.abs(x) @ np.abs(wt).T
+        assert (np.abs(down(out) - want) <= 1e-6 * scale + 1e-30).all()
+        b = rng.standard_normal(out_dim).astype(np.float32)
+        before = down(out)
+        K.add_bias_rows(out, up_f32(b), out_dim, n_tok)
+        assert np.array_equal(down(out), oracle.add_bias_rows(before, b, out_dim, n_tok))
