@@ -5,9 +5,10 @@
 // >= the unit count, capped at 64), so a wave holds rpp = 64 / lpr rows.
 // Lane `lir` of a row owns units lir, lir + lpr, lir + 2 lpr, ... (UPLMAX
 // at most). The four lanes of a super-block are adjacent, their exact
-// int32 partials meet in a 2-step DPP butterfly, and the super-block's fp32
-// value is formed on unit 0 in the reference's operation order. Those values
-// are then summed over the row's lanes in a fixed fp32 tree.
+// int32 partials meet in a 2-step DPP butterfly, and every lane of the quad
+// forms the super-block's fp32 value in the reference's operation order.
+// The quads' values are then summed over the row's lanes in a fixed fp32
+// tree.
 #pragma once
 
 #include "pk_formats.h"
@@ -49,13 +50,16 @@ PK_DEV void load_unit_act(const pulsar_block_q8_K *xq_row, uint32_t g, Act &a) {
     load_act<Fmt<Q>::kStride32, Fmt<Q>::kBsMode>(xq_row, g, a);
 }
 
-// Loads this lane's activation slices (UPLMAX units) of one q8_K row.
+// Loads this lane's activation slices (UPLMAX units) of one q8_K row. A
+// slice is loaded whenever its super-block exists, also for the missing
+// units of a MXFP4 tail super-block: q8_K blocks are always whole (their
+// tail is zero), and the quad's epilogue needs the block scale on every lane.
 template <uint32_t Q, uint32_t UPLMAX>
 PK_DEV void load_row_acts(const pulsar_block_q8_K *xq_row, const RowGeom &rg, Act (&a)[UPLMAX]) {
 #pragma unroll
     for (uint32_t i = 0; i < UPLMAX; i++) {
         const uint32_t g = rg.lir + (i << rg.lpr_log2);
-        if (g < rg.n_units) load_unit_act<Q>(xq_row, g, a[i]);
+        if ((g & ~3u) < rg.n_units) load_unit_act<Q>(xq_row, g, a[i]);
     }
 }
 
@@ -70,8 +74,10 @@ PK_DEV void load_row_w(const uint8_t *row, bool row_ok, const RowGeom &rg,
     }
 }
 
-// This lane's share of the row value: super-block values summed on unit-0
-// lanes (0 elsewhere). All lanes must call it (it exchanges across lanes).
+// This lane's share of the row value: every lane of a super-block's quad
+// ends with that super-block's value (the quad's integer sums meet in the
+// butterfly, and each lane forms the same fp32 epilogue from them). All
+// lanes must call it (it exchanges across lanes).
 template <uint32_t Q, uint32_t UPLMAX>
 PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::W (&w)[UPLMAX],
                          const Act (&a)[UPLMAX], const uint2 *lut) {
@@ -81,18 +87,21 @@ PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::
         const uint32_t g = rg.lir + (i << rg.lpr_log2);
         if ((i << rg.lpr_log2) >= rg.n_units) break;  // uniform: no unit of this lane set exists
         const bool ok = row_ok && g < rg.n_units;
+        // the super-block exists when its first unit does (a MXFP4 tail
+        // super-block may hold fewer than 4 units)
+        const bool sb_ok = row_ok && (g & ~3u) < rg.n_units;
         Part p = {0, 0, 0.0f};
         if (ok) p = Fmt<Q>::part(w[i], a[i], g & 3u, lut);
         p.i0 = group_sum<4>(p.i0);
         p.i1 = group_sum<4>(p.i1);
         if (Q == PULSAR_QUANT_MXFP4) p.f = group_sum<4>(p.f);
-        if (ok && (g & 3u) == 0u) acc += Fmt<Q>::sb_value(w[i], a[i].yd, p);
+        if (sb_ok) acc += Fmt<Q>::sb_value(w[i], a[i].yd, p);
     }
     return acc;
 }
 
-// Completes the row value across the row's lanes (result in every lane of
-// the row group).
+// Completes the row value across the row's lanes, starting from quads that
+// each hold one value (result in every lane of the row group).
 PK_DEV float row_finish(float acc, const RowGeom &rg) {
     return group_sum_from(acc, 4u, 1u << rg.lpr_log2);
 }
