@@ -154,6 +154,61 @@ int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32_t in_dim,
  * pulsar_add_bias_rows (pulsar_kernels.cu:3631). */
 int pulsar_add_bias_rows(void *x, const void *bias, uint32_t dim, uint32_t rows);
 
+/* ---- device-side routing (no counterpart entry point in the reference) ----
+ * The reference builds the per-(token, slot) pointer array and the grouped
+ * CSR on the host after reading the router's ids back
+ * (crates/engine/src/lib.rs:7663-7670, 8255-8344, 8357-8392). These two
+ * entry points do the same on the device, so a layer needs no host round
+ * trip. */
+
+/* One resident expert bank per projection: expert e's matrix starts at
+ * base + e * stride bytes; its bias (NULL base = none) at b_base + e * b_stride
+ * floats. Passed by host pointer, read at launch. */
+typedef struct pulsar_expert_bank {
+    const void *gate;
+    const void *up;
+    const void *down;
+    const float *gate_b;
+    const float *up_b;
+    const float *down_b;
+    uint64_t gate_stride;
+    uint64_t up_stride;
+    uint64_t down_stride;
+    uint64_t gate_b_stride;
+    uint64_t up_b_stride;
+    uint64_t down_b_stride;
+} pulsar_expert_bank;
+
+/* ptrs[t][s] / slot_weights[t][s] for s < k_used from the router's
+ * selected ids and weights ([n_tok][k_used]); an id outside [0, n_expert)
+ * gives a NULL slot. Then n_shared always-on slots (s = k_used + i) with
+ * pointers shared[i] (host array) and weight 1. Row stride of both outputs
+ * is k_used + n_shared. Replaces the host pointer build at
+ * crates/engine/src/lib.rs:8255-8344. */
+int pulsar_moe_route_ptrs(void *ptrs, void *slot_weights, const void *selected,
+                          const void *router_weights, const pulsar_expert_bank *bank,
+                          uint32_t n_expert, const pulsar_expert_ptrs *shared,
+                          uint32_t n_shared, uint32_t n_tok, uint32_t k_used);
+
+/* Groups the (token, slot) pairs of ptrs [n_tok][n_used] by expert (equal
+ * gate pointer, groups in order of first appearance, members in (token,
+ * slot) order; NULL gates skipped), as crates/engine/src/lib.rs:8357-8392
+ * does on the host. Writes gptrs [max_groups], starts [max_groups + 1] and
+ * pairs (token << 4 | slot); group slots past the real count get NULL
+ * pointers and empty ranges, so the grouped kernels can always be launched
+ * with n_group = max_groups (which must be at least the number of distinct
+ * experts, e.g. min(n_expert, n_tok * n_used)). n_used <= 16,
+ * n_tok * n_used <= 2048. */
+int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, const void *ptrs,
+                         uint32_t n_tok, uint32_t n_used, uint32_t max_groups);
+
+/* Selects the stream every later launch from the calling thread goes to
+ * (NULL restores the null stream, the default). No counterpart in the
+ * reference, whose launches always use the per-thread default stream
+ * (crates/kernels/build.rs:42-48); it lets a caller capture the path into a
+ * HIP graph on a capture stream. Returns 1. */
+int pulsar_set_stream(void *stream);
+
 /* Streaming-read probe: reads `bytes` (a multiple of 16) from buf through
  * the compute units; `sink` receives nothing unless the data sums to an
  * impossible value. Replaces pulsar_bw_read (pulsar_kernels.cu:4889). */

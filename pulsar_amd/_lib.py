@@ -32,6 +32,9 @@ SIGNATURES = {
     "pulsar_matmul_f32": [_vp, _vp, _vp, _u32, _u32, _u32],
     "pulsar_add_bias_rows": [_vp, _vp, _u32, _u32],
     "pulsar_bw_read": [_vp, _u64, _vp],
+    "pulsar_moe_route_ptrs": [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32],
+    "pulsar_moe_group_csr": [_vp, _vp, _vp, _vp, _u32, _u32, _u32],
+    "pulsar_set_stream": [_vp],
 }
 
 _lib: ctypes.CDLL | None = None

@@ -57,7 +57,7 @@ static void launch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K 
     // each wave loops
     const uint32_t waves = n_pass < 8192u ? n_pass : 8192u;
     const dim3 grid((waves + 3u) / 4u, (n_tok + T - 1u) / T);
-    hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX>), grid, dim3(256), 0, 0, out, w, xq, n_units,
+    hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX>), grid, dim3(256), 0, pk::stream(), out, w, xq, n_units,
                        nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
 }
 

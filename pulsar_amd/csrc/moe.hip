@@ -254,7 +254,7 @@ struct PairLaunch {
     int run() {
         const uint32_t rpb = kWaves * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_used, n_tok);
-        hipLaunchKernelGGL((moe_pair_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)mid,
+        hipLaunchKernelGGL((moe_pair_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)mid,
                            (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
                            (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
                            mid_dim, n_used, row_bytes, act_op);
@@ -272,7 +272,7 @@ struct DownLaunch {
     int run() {
         const uint32_t rpp = 64u >> g.l2;
         const dim3 grid((out_dim + rpp - 1u) / rpp, n_tok);
-        hipLaunchKernelGGL((moe_down_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)out,
+        hipLaunchKernelGGL((moe_down_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)out,
                            (const pulsar_expert_ptrs *)ptrs, (const pulsar_block_q8_K *)midq,
                            g.n_units, g.nblk32, g.l2, g.blocks, out_dim, n_used, row_bytes);
         return launch_ok("moe down launch");
@@ -289,7 +289,7 @@ struct PairGroupedLaunch {
     int run() {
         const uint32_t rpb = kWaves * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_group);
-        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), 0, 0, (float *)mid,
+        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)mid,
                            (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts,
                            (const uint32_t *)pairs, (const float *)weights,
                            (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
@@ -308,7 +308,7 @@ struct DownGroupedLaunch {
     int run() {
         const uint32_t rpb = kWaves * (64u >> g.l2);
         const dim3 grid((out_dim + rpb - 1u) / rpb, n_group);
-        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), 0, 0,
+        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), 0, pk::stream(),
                            (float *)partial, (const pulsar_expert_ptrs *)gptrs,
                            (const uint32_t *)starts, (const uint32_t *)pairs,
                            (const pulsar_block_q8_K *)midq, g.n_units, g.nblk32, g.l2, g.blocks,
@@ -385,7 +385,7 @@ extern "C" int pulsar_moe_slot_sum(void *out, const void *partial, uint32_t out_
                                    uint32_t n_tok) {
     if (!out || !partial || out_dim == 0 || n_used == 0 || n_tok == 0) return reject("moe slot sum");
     const uint64_t total = (uint64_t)n_tok * out_dim;
-    hipLaunchKernelGGL(slot_sum_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, 0,
+    hipLaunchKernelGGL(slot_sum_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, pk::stream(),
                        (float *)out, (const float *)partial, out_dim, n_used, total);
     return launch_ok("moe slot sum launch");
 }
@@ -395,7 +395,7 @@ extern "C" int pulsar_moe_down_bias(void *out, const void *ptrs, const void *wei
     if (!out || !ptrs || !weights || out_dim == 0 || n_used == 0 || n_tok == 0)
         return reject("moe down bias");
     const uint64_t total = (uint64_t)n_tok * out_dim;
-    hipLaunchKernelGGL(down_bias_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, 0,
+    hipLaunchKernelGGL(down_bias_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, pk::stream(),
                        (float *)out, (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
                        out_dim, n_used, total);
     return launch_ok("moe down bias launch");

@@ -17,6 +17,10 @@ namespace pk {
 
 constexpr uint32_t kWave = 64;
 
+// Stream of every launch made by the calling thread (pulsar_set_stream;
+// the null stream by default, like the reference's launches).
+hipStream_t stream();
+
 // Error reporting with the reference's message shape (pulsar_kernels.cu:25-29).
 static inline int launch_ok(const char *what) {
     const hipError_t err = hipGetLastError();

@@ -3,6 +3,9 @@
 
 namespace pk {
 
+static thread_local hipStream_t g_stream = nullptr;
+hipStream_t stream() { return g_stream; }
+
 // One wave per 256-value block; lane l owns values 4l .. 4l+3.
 // Algorithm of the CPU lane (crates/quant/src/cpu_dot.rs:26-50):
 //   amax = max |x|; amax == 0 -> d = 0, all quants 0;
@@ -80,14 +83,19 @@ extern "C" int pulsar_quantize_q8_K(void *out, const void *x, uint32_t in_dim, u
     const uint64_t n_blocks = (uint64_t)nb * n_rows;
     const uint64_t grid = (n_blocks + 3u) / 4u;
     if (grid > 0x7fffffffull) return pk::reject("q8_K quantize");
-    hipLaunchKernelGGL(pk::quantize_q8k_kernel, dim3((uint32_t)grid), dim3(256), 0, 0,
+    hipLaunchKernelGGL(pk::quantize_q8k_kernel, dim3((uint32_t)grid), dim3(256), 0, pk::stream(),
                        (pulsar_block_q8_K *)out, (const float *)x, in_dim, nb, n_blocks);
     return pk::launch_ok("q8_K quantize launch");
 }
 
 extern "C" int pulsar_bw_read(void *buf, uint64_t bytes, void *sink) {
     if (!buf || !sink || bytes < 16) return pk::reject("bw_read");
-    hipLaunchKernelGGL(pk::bw_read_kernel, dim3(4096), dim3(256), 0, 0, (const pk::u32x4 *)buf,
+    hipLaunchKernelGGL(pk::bw_read_kernel, dim3(4096), dim3(256), 0, pk::stream(), (const pk::u32x4 *)buf,
                        bytes / 16u, (float *)sink);
     return pk::launch_ok("bw_read launch");
+}
+
+extern "C" int pulsar_set_stream(void *stream) {
+    pk::g_stream = (hipStream_t)stream;
+    return 1;
 }

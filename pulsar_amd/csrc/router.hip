@@ -167,7 +167,7 @@ __global__ __launch_bounds__(64) void router_select_kernel(int32_t *__restrict__
 extern "C" int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32_t in_dim,
                                  uint32_t out_dim, uint32_t n_tok) {
     if (!out || !w || !x || in_dim == 0 || out_dim == 0 || n_tok == 0) return pk::reject("matmul f32");
-    hipLaunchKernelGGL(pk::matmul_f32_kernel, dim3(out_dim), dim3(64), 0, 0, (float *)out,
+    hipLaunchKernelGGL(pk::matmul_f32_kernel, dim3(out_dim), dim3(64), 0, pk::stream(), (float *)out,
                        (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
     return pk::launch_ok("matmul f32 launch");
 }
@@ -176,7 +176,7 @@ extern "C" int pulsar_add_bias_rows(void *x, const void *bias, uint32_t dim, uin
     if (!x || !bias || dim == 0 || rows == 0) return pk::reject("add bias rows");
     const uint64_t total = (uint64_t)rows * dim;
     hipLaunchKernelGGL(pk::add_bias_rows_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256),
-                       0, 0, (float *)x, (const float *)bias, dim, total);
+                       0, pk::stream(), (float *)x, (const float *)bias, dim, total);
     return pk::launch_ok("add bias rows launch");
 }
 
@@ -189,7 +189,7 @@ extern "C" int pulsar_router_select(void *selected, void *weights, const void *l
         n_tok == 0 || softmax_mode > 2u || (softmax_mode != 2u && n_shexp != 0) ||
         n_expert + (softmax_mode == 2u ? n_shexp : 0u) > 1024u || n_expert > 64u * pk::kMaxPerLane)
         return pk::reject("router select");
-    hipLaunchKernelGGL(pk::router_select_kernel, dim3(n_tok), dim3(64), 0, 0, (int32_t *)selected,
+    hipLaunchKernelGGL(pk::router_select_kernel, dim3(n_tok), dim3(64), 0, pk::stream(), (int32_t *)selected,
                        (float *)weights, (const float *)logits, (const float *)bias, n_expert, k_used,
                        weight_scale, softmax_mode, n_shexp);
     return pk::launch_ok("router select launch");

@@ -9,6 +9,8 @@ reference's kernels::sync) before reading results on the host.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from . import _lib
@@ -115,6 +117,56 @@ def router_select(selected, weights, logits, bias, n_expert: int, k_used: int, w
 
 def matmul_f32(out, w, x, in_dim: int, out_dim: int, n_tok: int) -> None:
     _check(_lib.load().pulsar_matmul_f32(_ptr(out), _ptr(w), _ptr(x), in_dim, out_dim, n_tok), "matmul_f32")
+
+
+class ExpertBank(ctypes.Structure):
+    """pulsar_expert_bank (include/pulsar_moe.h): expert e's projection starts
+    at base + e * stride bytes, its bias at b_base + e * b_stride floats."""
+
+    _fields_ = [
+        ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p),
+        ("gate_b", ctypes.c_void_p), ("up_b", ctypes.c_void_p), ("down_b", ctypes.c_void_p),
+        ("gate_stride", ctypes.c_uint64), ("up_stride", ctypes.c_uint64), ("down_stride", ctypes.c_uint64),
+        ("gate_b_stride", ctypes.c_uint64), ("up_b_stride", ctypes.c_uint64), ("down_b_stride", ctypes.c_uint64),
+    ]
+
+
+class _Ptrs6(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("gate", "up", "down", "gate_b", "up_b", "down_b")]
+
+
+def moe_route_ptrs(ptrs, slot_weights, selected, router_weights, bank: ExpertBank, n_expert: int,
+                   shared, n_tok: int, k_used: int) -> None:
+    """Device-side pointer build (no reference counterpart entry point; it
+    replaces the host build of crates/engine/src/lib.rs:8255-8344).
+    `shared` is a list of (gate, up, down[, biases]) address tuples."""
+    shared = list(shared or [])
+    arr = (_Ptrs6 * max(1, len(shared)))()
+    for i, e in enumerate(shared):
+        e = tuple(e) + (0,) * (6 - len(e))
+        arr[i] = _Ptrs6(*[int(v) or None for v in e])
+    _check(
+        _lib.load().pulsar_moe_route_ptrs(_ptr(ptrs), _ptr(slot_weights), _ptr(selected), _ptr(router_weights),
+                                          ctypes.byref(bank), n_expert, ctypes.cast(arr, ctypes.c_void_p),
+                                          len(shared), n_tok, k_used),
+        "moe_route_ptrs",
+    )
+
+
+def moe_group_csr(gptrs, starts, pairs, ptrs, n_tok: int, n_used: int, max_groups: int) -> None:
+    """Device-side CSR by expert (replaces crates/engine/src/lib.rs:8357-8392)."""
+    _check(
+        _lib.load().pulsar_moe_group_csr(_ptr(gptrs), _ptr(starts), _ptr(pairs), _ptr(ptrs), n_tok, n_used,
+                                         max_groups),
+        "moe_group_csr",
+    )
+
+
+def set_stream(stream) -> None:
+    """Routes later launches from this thread to `stream` (a torch Stream, a
+    raw hipStream_t int, or None for the null stream)."""
+    handle = 0 if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+    _check(_lib.load().pulsar_set_stream(handle or None), "set_stream")
 
 
 def bw_read(buf, nbytes: int, sink) -> None:

@@ -224,3 +224,87 @@ def test_matmul_f32_and_bias(dev):
         before = down(out)
         K.add_bias_rows(out, up_f32(b), out_dim, n_tok)
         assert np.array_equal(down(out), oracle.add_bias_rows(before, b, out_dim, n_tok))
+
+
+# ------------------------------------------------- device routing, graphs --
+
+def test_route_ptrs_and_group_csr(dev):
+    E, k, n_tok, hidden, ffn = 12, 6, 20, 256, 256
+    L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=hidden, ffn=ffn, E=E, n_used=k, n_tok=n_tok, biases=True)
+    sel = rng.integers(0, E, (n_tok, k)).astype(np.int32)
+    sel[3, 2] = -1  # unrouted
+    sel[7, 0] = E + 5  # out of range -> NULL
+    rw = rng.uniform(0.1, 1, (n_tok, k)).astype(np.float32)
+    gsz, dsz = ffn * L.grb, hidden * L.drb
+    bank = K.ExpertBank(L.dg.data_ptr(), L.du.data_ptr(), L.dd.data_ptr(), L.dbias[0].data_ptr(),
+                        L.dbias[1].data_ptr(), L.dbias[2].data_ptr(), gsz, gsz, dsz, ffn, ffn, hidden)
+    shared = (11 << 20, 12 << 20, 13 << 20)  # opaque addresses: only copied, never dereferenced
+    n_slots = k + 1
+    ptrs = torch.zeros(n_tok * n_slots * 48, dtype=torch.uint8, device=dev)
+    slot_w = zeros_f32((n_tok, n_slots))
+    K.moe_route_ptrs(ptrs, slot_w, up(sel), up_f32(rw), bank, E, [shared], n_tok, k)
+    got = down(ptrs).view(K.EXPERT_PTRS_DTYPE).reshape(n_tok, n_slots)
+    want_w = np.concatenate([rw, np.ones((n_tok, 1), np.float32)], axis=1)
+    assert np.array_equal(down(slot_w), want_w)
+    for t in range(n_tok):
+        for s in range(n_slots):
+            if s == k:
+                want = shared + (0, 0, 0)
+            elif 0 <= sel[t, s] < E:
+                want = L.dev_entries(int(sel[t, s]))
+            else:
+                want = (0,) * 6
+            assert tuple(int(v) for v in got[t, s]) == tuple(want), (t, s)
+    # CSR by gate pointer, first appearance order, NULL gates skipped
+    max_groups = E + 1
+    gptrs = torch.zeros(max_groups * 48, dtype=torch.uint8, device=dev)
+    starts = torch.zeros(max_groups + 1, dtype=torch.int32, device=dev)
+    pairs = torch.zeros(n_tok * n_slots, dtype=torch.int32, device=dev)
+    K.moe_group_csr(gptrs, starts, pairs, ptrs, n_tok, n_slots, max_groups)
+    ids = np.concatenate([np.where((sel >= 0) & (sel < E), sel, -1), np.full((n_tok, 1), E)], axis=1)
+    want_ids, want_starts, want_pairs = synth.csr_by_expert(ids, n_slots)
+    g = down(gptrs).view(K.EXPERT_PTRS_DTYPE)
+    ng = len(want_ids)
+    assert np.array_equal(down(starts)[:ng + 1], want_starts)
+    assert (down(starts)[ng:] == want_starts[-1]).all()
+    assert np.array_equal(down(pairs)[:len(want_pairs)].astype(np.uint32), want_pairs)
+    for gi, e in enumerate(want_ids):
+        want = shared + (0, 0, 0) if e == E else L.dev_entries(int(e))
+        assert tuple(int(v) for v in g[gi]) == tuple(want)
+    assert not g[ng:].view(np.uint64).any()
+
+
+def test_graph_replays_match_eager(dev):
+    """The pair/quantize/down chain captured into a HIP graph on a capture
+    stream (pulsar_set_stream) and replayed three times, with eager work in
+    between, reproduces the eager result bit for bit every time."""
+    L = Layer(QUANT_Q4_K, QUANT_Q6_K, hidden=2048, ffn=512, E=10, n_used=9, n_tok=1)
+    _, dptrs = L.ptrs()
+    xq = up(oracle.quantize_q8_k(L.x))
+    w = up_f32(L.w)
+    mid = zeros_f32((L.n_used, L.ffn))
+    midq = torch.zeros(L.n_used * 2 * 292, dtype=torch.uint8, device=dev)
+    out = zeros_f32((1, L.hidden))
+
+    def chain():
+        K.moe_pair_swiglu(mid, dptrs, w, xq, L.hidden, L.ffn, L.n_used, 1, L.grb, L.gq, ACT_SILU)
+        K.quantize_q8_k(midq, mid, L.ffn, L.n_used)
+        K.moe_down(out, dptrs, midq, L.ffn, L.hidden, L.n_used, 1, L.drb, L.dq)
+
+    chain()
+    eager = down(out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        K.set_stream(torch.cuda.current_stream())
+        try:
+            chain()
+        finally:
+            K.set_stream(None)
+    for _ in range(3):
+        out.zero_()
+        mid.fill_(123.0)
+        torch.cuda.synchronize()
+        g.replay()
+        assert np.array_equal(down(out), eager)
+        chain()  # eager work between replays
+        assert np.array_equal(down(out), eager)
