@@ -9,7 +9,11 @@
 
 namespace pk {
 
-template <uint32_t Q, uint32_t T, uint32_t UPLMAX>
+// Each wave streams row passes pass0, pass0 + n_waves, ...: the row's
+// weight units are requested first, then (once per wave) the token's
+// activation slices, so the HBM latency of the first row overlaps the L2
+// latency of the activations.
+template <uint32_t Q, uint32_t T, uint32_t UPLMAX, uint32_t RPW, uint32_t L2>
 __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
                                                      const uint8_t *__restrict__ w,
                                                      const pulsar_block_q8_K *__restrict__ xq,
@@ -22,6 +26,64 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
         fill_iq2xxs_lut(lut);
         __syncthreads();
     }
+    const RowGeom rg = row_geom<L2>(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> rg.lpr_log2;
+    const uint32_t t0 = blockIdx.y * T;
+    const uint32_t waves = blockDim.x / 64u;
+    const uint32_t n_waves = gridDim.x * waves;
+    uint32_t base = (blockIdx.x * waves + threadIdx.x / 64u) * RPW;
+    if (base >= n_pass) return;  // whole wave
+    typename Fmt<Q>::W wu[RPW][UPLMAX];
+#pragma unroll
+    for (uint32_t p = 0; p < RPW; p++) {
+        const uint32_t row = (base + p) * rpp + rg.rip;
+        load_row_w<Q, UPLMAX>(w + (uint64_t)(row < out_dim ? row : 0u) * row_bytes, rg, wu[p]);
+    }
+    Act a[T][UPLMAX];
+#pragma unroll
+    for (uint32_t t = 0; t < T; t++) {
+        const uint32_t tok = t0 + t < n_tok ? t0 + t : n_tok - 1u;
+        load_row_acts<Q, UPLMAX>(xq + (uint64_t)tok * in_blocks, rg, a[t]);
+    }
+    for (;;) {
+#pragma unroll
+        for (uint32_t p = 0; p < RPW; p++) {
+            const uint32_t row = (base + p) * rpp + rg.rip;
+            const bool row_ok = row < out_dim;
+#pragma unroll
+            for (uint32_t t = 0; t < T; t++) {
+                float acc = row_partial<Q, UPLMAX>(row_ok, rg, wu[p], a[t], lut);
+                acc = row_finish(acc, rg);
+                if (row_ok && rg.holds_row() && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = acc;
+            }
+        }
+        base += n_waves * RPW;
+        if (base >= n_pass) break;
+#pragma unroll
+        for (uint32_t p = 0; p < RPW; p++) {
+            const uint32_t row = (base + p) * rpp + rg.rip;
+            load_row_w<Q, UPLMAX>(w + (uint64_t)(row < out_dim ? row : 0u) * row_bytes, rg, wu[p]);
+        }
+    }
+}
+
+// LDS-tiled variant: the block stages `tile_rows` consecutive rows (one
+// contiguous byte span of the matrix) with dense 16-byte loads - every
+// wave-wide load instruction reads 1 KiB of whole cache lines - then each
+// wave decodes its row passes from LDS with the same unit decoders.
+constexpr uint32_t kTileMax = 32768;  // bytes of one staged tile
+
+template <uint32_t Q, uint32_t T, uint32_t UPLMAX>
+__global__ __launch_bounds__(256) void matvec_lds_kernel(float *__restrict__ out,
+                                                         const uint8_t *__restrict__ w,
+                                                         const pulsar_block_q8_K *__restrict__ xq,
+                                                         uint32_t n_units, uint32_t nblk32,
+                                                         uint32_t lpr_log2, uint32_t in_blocks,
+                                                         uint32_t out_dim, uint32_t n_tok,
+                                                         uint64_t row_bytes, uint32_t tile_rows) {
+    __shared__ uint2 lut[Q == PULSAR_QUANT_IQ2_XXS ? 256 : 1];
+    __shared__ uint4 tile[kTileMax / 16 + 1];
+    if (Q == PULSAR_QUANT_IQ2_XXS) fill_iq2xxs_lut(lut);
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t t0 = blockIdx.y * T;
@@ -31,35 +93,71 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
         const uint32_t tok = t0 + t < n_tok ? t0 + t : n_tok - 1u;
         load_row_acts<Q, UPLMAX>(xq + (uint64_t)tok * in_blocks, rg, a[t]);
     }
-    const uint32_t waves = blockDim.x / 64u;
-    const uint32_t n_waves = gridDim.x * waves;
-    for (uint32_t pass = blockIdx.x * waves + threadIdx.x / 64u; pass < n_pass; pass += n_waves) {
-        const uint32_t row = pass * rpp + rg.rip;
-        const bool row_ok = row < out_dim;
-        typename Fmt<Q>::W wu[UPLMAX];
-        load_row_w<Q, UPLMAX>(w + (uint64_t)row * row_bytes, row_ok, rg, wu);
+    const uint32_t wave = threadIdx.x / 64u;
+    const uint32_t n_tiles = (out_dim + tile_rows - 1u) / tile_rows;
+    const uint32_t passes = tile_rows / rpp;  // a multiple of the 4 waves
+    for (uint32_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x) {
+        const uint32_t r0 = ti * tile_rows;
+        const uint32_t nr = out_dim - r0 < tile_rows ? out_dim - r0 : tile_rows;
+        const uint64_t start = (uint64_t)r0 * row_bytes;
+        const uint64_t end = start + (uint64_t)nr * row_bytes;
+        // 16-byte granules covering [start, end): the first may begin up to
+        // 15 bytes early and the last end up to 15 bytes late, both inside
+        // the granules (hence the pages) the rows themselves occupy
+        const uintptr_t g0 = ((uintptr_t)(w + start)) & ~(uintptr_t)15;
+        const uint32_t shift = (uint32_t)((uintptr_t)(w + start) - g0);
+        const uint32_t n16 = (uint32_t)((shift + (end - start) + 15u) / 16u);
+        __syncthreads();  // the previous tile's readers are done
+        for (uint32_t c = threadIdx.x; c < n16; c += blockDim.x) tile[c] = *(const uint4 *)(g0 + 16u * c);
+        __syncthreads();
+        const uint8_t *tb = (const uint8_t *)tile + shift;
+        for (uint32_t p = wave; p < passes; p += 4u) {
+            const uint32_t rl = p * rpp + rg.rip;
+            const bool row_ok = rl < nr;
+            typename Fmt<Q>::W wu[UPLMAX];
+            load_row_w<Q, UPLMAX>(tb + (uint64_t)(row_ok ? rl : 0u) * row_bytes, rg, wu);
 #pragma unroll
-        for (uint32_t t = 0; t < T; t++) {
-            float acc = row_partial<Q, UPLMAX>(row_ok, rg, wu, a[t], lut);
-            acc = row_finish(acc, rg);
-            if (row_ok && rg.lir == 0 && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = acc;
+            for (uint32_t t = 0; t < T; t++) {
+                float acc = row_partial<Q, UPLMAX>(row_ok, rg, wu, a[t], lut);
+                acc = row_finish(acc, rg);
+                if (row_ok && rg.holds_row() && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + r0 + rl] = acc;
+            }
         }
     }
 }
 
-template <uint32_t Q, uint32_t T, uint32_t UPLMAX>
+#ifndef PK_MV_RPW
+#define PK_MV_RPW 1
+#endif
+#ifndef PK_MV_WAVES
+#define PK_MV_WAVES 4096u
+#endif
+#ifndef PK_MV_TILE
+#define PK_MV_TILE 16384u
+#endif
+#ifndef PK_MV_BLOCKS
+#define PK_MV_BLOCKS 2048u
+#endif
+
+template <uint32_t Q, uint32_t T, uint32_t UPLMAX, uint32_t RPW>
 static void launch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t n_units,
                           uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t out_dim,
                           uint32_t n_tok, uint64_t row_bytes) {
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t n_pass = (out_dim + rpp - 1u) / rpp;
-    // one wave per row pass up to 8192 waves (8 per SIMD on 256 CUs), then
-    // each wave loops
-    const uint32_t waves = n_pass < 8192u ? n_pass : 8192u;
+    // waves capped at PK_MV_WAVES (a few per SIMD on 256 CUs); larger
+    // matrices loop
+    const uint32_t chunks = (n_pass + RPW - 1u) / RPW;
+    const uint32_t waves = chunks < PK_MV_WAVES ? chunks : PK_MV_WAVES;
     const dim3 grid((waves + 3u) / 4u, (n_tok + T - 1u) / T);
-    hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX>), grid, dim3(256), 0, pk::stream(), out, w, xq, n_units,
-                       nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
+    if (lpr_log2 == 6)
+        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 6>), grid, dim3(256), 0, pk::stream(), out, w, xq,
+                           n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
+    else
+        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 0>), grid, dim3(256), 0, pk::stream(), out, w, xq,
+                           n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
 }
+
 
 template <uint32_t Q>
 static int dispatch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
@@ -69,25 +167,44 @@ static int dispatch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K
     const uint32_t upl = (n_units + (1u << l2) - 1u) >> l2;
     const uint32_t in_blocks = (in_dim + 255u) / 256u;
     const uint32_t nblk32 = (in_dim + 31u) / 32u;
+#ifdef PK_MV_LDS
+    {
+        const uint32_t rpp = 64u >> l2;
+        uint32_t tile_rows = (uint32_t)(PK_MV_TILE / row_bytes) / (4u * rpp) * (4u * rpp);
+        if (tile_rows >= 4u * rpp && upl <= 1u && n_tok <= 2u) {
+            const uint32_t n_tiles = (out_dim + tile_rows - 1u) / tile_rows;
+            const uint32_t grid = n_tiles < PK_MV_BLOCKS ? n_tiles : PK_MV_BLOCKS;
+            if (n_tok == 1u)
+                hipLaunchKernelGGL((matvec_lds_kernel<Q, 1, 1>), dim3(grid, 1), dim3(256), 0, pk::stream(), out, w,
+                                   xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes, tile_rows);
+            else
+                hipLaunchKernelGGL((matvec_lds_kernel<Q, 2, 1>), dim3(grid, 1), dim3(256), 0, pk::stream(), out, w,
+                                   xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes, tile_rows);
+            return launch_ok("matmul_kq launch");
+        }
+    }
+#endif
+#define PK_MV(T, U, R) launch_matvec<Q, T, U, R>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes)
     if (upl <= 1u) {
         if (n_tok == 1u)
-            launch_matvec<Q, 1, 1>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+            PK_MV(1, 1, PK_MV_RPW);
         else if (n_tok == 2u)
-            launch_matvec<Q, 2, 1>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+            PK_MV(2, 1, 2);
         else
-            launch_matvec<Q, 4, 1>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+            PK_MV(4, 1, 1);
     } else if (upl <= 2u) {
         if (n_tok == 1u)
-            launch_matvec<Q, 1, 2>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+            PK_MV(1, 2, 2);
         else
-            launch_matvec<Q, 2, 2>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+            PK_MV(2, 2, 1);
     } else if (upl <= 4u) {
-        launch_matvec<Q, 1, 4>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+        PK_MV(1, 4, 1);
     } else if (upl <= 8u) {
-        launch_matvec<Q, 1, 8>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes);
+        PK_MV(1, 8, 1);
     } else {
         return reject("matmul_kq (in_dim above 32768)");
     }
+#undef PK_MV
     return launch_ok("matmul_kq launch");
 }
 

@@ -42,17 +42,17 @@ __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
     const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
     const bool row_ok = row < mid_dim;
     if (!p.gate || !p.up) {  // unrouted slot contributes zero (pulsar_kernels.cu:2587-2590)
-        if (row_ok && rg.lir == 0) mid[so * mid_dim + row] = 0.0f;
+        if (row_ok && rg.holds_row()) mid[so * mid_dim + row] = 0.0f;
         return;
     }
     Act a[UPLMAX];
     load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
     typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)row * row_bytes, row_ok, rg, wg);
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)row * row_bytes, row_ok, rg, wu);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
     float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
     float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
-    if (row_ok && rg.lir == 0) {
+    if (row_ok && rg.holds_row()) {
         // bias on the projection output, then the combine, then the router
         // weight (pulsar_kernels.cu:2606-2612)
         if (p.gate_b) g += p.gate_b[row];
@@ -90,17 +90,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                 Act a[UPLMAX];
                 load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
                 typename Fmt<Q>::W w[UPLMAX];
-                load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)row * row_bytes, row_ok, rg, w);
+                load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
                 v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
             }
-            if (rg.lir == 0) part[s - base][rg.rip] = v;
+            if (rg.holds_row()) part[s - base][rg.rip] = v;
         }
         __syncthreads();
-        if (wave == 0 && rg.lir == 0)
+        if (wave == 0 && rg.holds_row())
             for (uint32_t s = base; s < end; s++) total += part[s - base][rg.rip];
         __syncthreads();
     }
-    if (wave == 0 && rg.lir == 0 && row_ok) out[(uint64_t)token * out_dim + row] = total;
+    if (wave == 0 && rg.holds_row() && row_ok) out[(uint64_t)token * out_dim + row] = total;
 }
 
 template <uint32_t Q, uint32_t UPLMAX>
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
     const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
     const bool row_ok = row < mid_dim;
     typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)row * row_bytes, row_ok, rg, wg);
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)row * row_bytes, row_ok, rg, wu);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
     const float gb = row_ok && p.gate_b ? p.gate_b[row] : 0.0f;
     const float ub = row_ok && p.up_b ? p.up_b[row] : 0.0f;
     const uint32_t s0 = starts[group], s1 = starts[group + 1];
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
         load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
         float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
         float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
-        if (row_ok && rg.lir == 0) {
+        if (row_ok && rg.holds_row()) {
             if (p.gate_b) g += gb;
             if (p.up_b) u += ub;
             mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
     const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
     const bool row_ok = row < out_dim;
     typename Fmt<Q>::W w[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)row * row_bytes, row_ok, rg, w);
+    load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
     const uint32_t s0 = starts[group], s1 = starts[group + 1];
     for (uint32_t i = s0; i < s1; i++) {
         const uint32_t pr = pairs[i];
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
         Act a[UPLMAX];
         load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
         const float v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
-        if (row_ok && rg.lir == 0) partial[so * out_dim + row] = v;
+        if (row_ok && rg.holds_row()) partial[so * out_dim + row] = v;
     }
 }
 

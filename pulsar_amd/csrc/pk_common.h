@@ -53,6 +53,25 @@ PK_DEV uint4 ld128(const uint8_t *p) {
     __builtin_memcpy(&v, p, 16);
     return v;
 }
+typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(1)));
+typedef uint32_t u32x2_u __attribute__((ext_vector_type(2), aligned(1)));
+// Streaming (read-once) weight loads: non-temporal hint, any alignment.
+PK_DEV uint4 ldw128(const uint8_t *p) {
+#ifdef PK_NT_LOADS
+    const u32x4_u v = __builtin_nontemporal_load((const u32x4_u *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return ld128(p);
+#endif
+}
+PK_DEV uint2 ldw64(const uint8_t *p) {
+#ifdef PK_NT_LOADS
+    const u32x2_u v = __builtin_nontemporal_load((const u32x2_u *)p);
+    return make_uint2(v.x, v.y);
+#else
+    return ld64(p);
+#endif
+}
 PK_DEV uint16_t ld16(const uint8_t *p) {
     uint16_t v;
     __builtin_memcpy(&v, p, 2);
@@ -103,6 +122,28 @@ template <typename T>
 PK_DEV T group_sum_from(T v, uint32_t from, uint32_t g) {
     for (uint32_t s = from; s < g; s <<= 1) v += partner(v, s);
     return v;
+}
+
+// Accumulating DPP moves for reductions that end in the LAST lane of each
+// group: row_shr:n reads lane i-n of the same 16-lane row (0 where that
+// lane is outside the row), row_bcast:15 / :31 add lane 15 / 31 of the
+// preceding row(s) into rows 1,3 / 2,3 (the other rows add 0).
+template <int N>
+PK_DEV float dpp_shr(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int32_t, v),
+                                                                 0x110 + N, 0xF, 0xF, true));
+}
+template <int N>
+PK_DEV int32_t dpp_shr(int32_t v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x110 + N, 0xF, 0xF, true);
+}
+PK_DEV float dpp_bcast15(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int32_t, v),
+                                                                 0x142, 0xA, 0xF, false));
+}
+PK_DEV float dpp_bcast31(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int32_t, v),
+                                                                 0x143, 0xC, 0xF, false));
 }
 
 PK_DEV int32_t lane_xor(int32_t v, uint32_t m) { return __shfl_xor(v, (int)m, 64); }

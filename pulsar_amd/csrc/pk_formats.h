@@ -100,6 +100,7 @@ struct Fmt;
 // scales[12] @4, qs[128] @16. Lane dot: cpu_dot.rs:250-279.
 template <>
 struct Fmt<PULSAR_QUANT_Q4_K> {
+    static constexpr bool kHasI1 = true;  // second exact sum (min terms) in use
     static constexpr uint32_t kSbBytes = 144;
     static constexpr bool kStride32 = false;
     static constexpr int kBsMode = 1;
@@ -111,9 +112,9 @@ struct Fmt<PULSAR_QUANT_Q4_K> {
         const uint8_t *blk = row + (uint64_t)(g >> 2) * kSbBytes;
         const uint32_t u = g & 3u;
         W w;
-        w.hdr = ld128(blk);
-        w.qa = ld128(blk + 16 + 32u * u);
-        w.qb = ld128(blk + 32 + 32u * u);
+        w.hdr = ldw128(blk);
+        w.qa = ldw128(blk + 16 + 32u * u);
+        w.qb = ldw128(blk + 32 + 32u * u);
         return w;
     }
     // get_scale_min_k4 (cpu_dot.rs:147-156) for j = 2u and 2u + 1
@@ -161,6 +162,7 @@ struct Fmt<PULSAR_QUANT_Q4_K> {
 // q8_K group sum: sum (c - 32) * x = sum c * x - 32 * bsum (exact).
 template <>
 struct Fmt<PULSAR_QUANT_Q6_K> {
+    static constexpr bool kHasI1 = false;  // second exact sum (min terms) in use
     static constexpr uint32_t kSbBytes = 210;
     static constexpr bool kStride32 = true;
     static constexpr int kBsMode = 2;
@@ -173,34 +175,38 @@ struct Fmt<PULSAR_QUANT_Q6_K> {
         const uint8_t *blk = row + (uint64_t)(g >> 2) * kSbBytes;
         const uint32_t u = g & 3u, h = u >> 1, k = u & 1u;
         W w;
-        w.la = ld128(blk + 64u * h + 16u * k);
-        w.lb = ld128(blk + 64u * h + 32u + 16u * k);
-        w.qh = ld128(blk + 128u + 32u * h + 16u * k);
-        w.sc = ld64(blk + 192u + 8u * h);
+        w.la = ldw128(blk + 64u * h + 16u * k);
+        w.lb = ldw128(blk + 64u * h + 32u + 16u * k);
+        w.qh = ldw128(blk + 128u + 32u * h + 16u * k);
+        w.sc = ldw64(blk + 192u + 8u * h);
         w.d = ld16(blk + 208u);
         return w;
     }
     PK_DEV static Part part(const W &w, const Act &a, uint32_t u, const uint2 *) {
         const uint32_t k = u & 1u;
-        const uint32_t lo = 0x0f0f0f0fu, m2 = 0x03030303u;
-        int32_t g[4];
+        const uint32_t lo4 = 0x0f0f0f0fu, hi2 = 0x30303030u;
+        // code c = low nibble | (2 high bits << 4): the high bits of quarter
+        // q sit at bits 2q..2q+1 of each qh byte and move to bits 4..5
+        const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        const uint32_t la[4] = {w.la.x, w.la.y, w.la.z, w.la.w};
+        const uint32_t lb[4] = {w.lb.x, w.lb.y, w.lb.z, w.lb.w};
+        uint32_t c[4][4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 l = (q & 1) ? w.lb : w.la;
-            const uint32_t ls = (q >> 1) ? 4u : 0u;
-            const uint32_t hs = 2u * q;
-            const uint32_t c0 = ((l.x >> ls) & lo) | (((w.qh.x >> hs) & m2) << 4);
-            const uint32_t c1 = ((l.y >> ls) & lo) | (((w.qh.y >> hs) & m2) << 4);
-            const uint32_t c2 = ((l.z >> ls) & lo) | (((w.qh.z >> hs) & m2) << 4);
-            const uint32_t c3 = ((l.w >> ls) & lo) | (((w.qh.w >> hs) & m2) << 4);
-            g[q] = dot16(c0, c1, c2, c3, a.q[q], 0) - 32 * a.bs[q];
+        for (int i = 0; i < 4; i++) {
+            c[0][i] = (la[i] & lo4) | ((qh[i] << 4) & hi2);
+            c[1][i] = (lb[i] & lo4) | ((qh[i] << 2) & hi2);
+            c[2][i] = ((la[i] >> 4) & lo4) | (qh[i] & hi2);
+            c[3][i] = ((lb[i] >> 4) & lo4) | ((qh[i] >> 2) & hi2);
         }
+        // scales of this unit: bytes k, k+2, k+4, k+6 of scales[8h..8h+7]
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(w.sc.y, w.sc.x, k);
+        const uint32_t s1 = __builtin_amdgcn_alignbyte(0u, w.sc.y, k);
+        const int32_t sc[4] = {(int32_t)(s0 << 24) >> 24, (int32_t)(s0 << 8) >> 24,
+                               (int32_t)(s1 << 24) >> 24, (int32_t)(s1 << 8) >> 24};
         int32_t isum = 0;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int32_t sc = (int32_t)(int8_t)byte_of(w.sc, 2u * q + k);
-            isum += sc * g[q];
-        }
+        for (int q = 0; q < 4; q++)
+            isum += sc[q] * (dot16(c[q][0], c[q][1], c[q][2], c[q][3], a.q[q], 0) - 32 * a.bs[q]);
         return Part{isum, 0, 0.0f};
     }
     // d * y->d * isum with d = x->d (pulsar_kernels.cu:5946)
@@ -217,6 +223,7 @@ struct Fmt<PULSAR_QUANT_Q6_K> {
 // by 2s gives values 128k + 32s + 16half + i under scale byte 8k + 2s + half.
 template <>
 struct Fmt<PULSAR_QUANT_Q2_K> {
+    static constexpr bool kHasI1 = true;  // second exact sum (min terms) in use
     static constexpr uint32_t kSbBytes = 84;
     static constexpr bool kStride32 = true;
     static constexpr int kBsMode = 2;
@@ -229,8 +236,8 @@ struct Fmt<PULSAR_QUANT_Q2_K> {
         const uint8_t *blk = row + (uint64_t)(g >> 2) * kSbBytes;
         const uint32_t u = g & 3u, k = u >> 1, half = u & 1u;
         W w;
-        w.qs = ld128(blk + 16u + 32u * k + 16u * half);
-        w.sc = ld64(blk + 8u * k);
+        w.qs = ldw128(blk + 16u + 32u * k + 16u * half);
+        w.sc = ldw64(blk + 8u * k);
         w.dd = ld32(blk + 80u);
         return w;
     }
@@ -276,6 +283,7 @@ PK_DEV void iq2_signed8(const uint2 *lut, uint32_t idx, uint32_t s7, uint32_t &w
 
 template <>
 struct Fmt<PULSAR_QUANT_IQ2_XXS> {
+    static constexpr bool kHasI1 = false;  // second exact sum (min terms) in use
     static constexpr uint32_t kSbBytes = 66;
     static constexpr bool kStride32 = false;
     static constexpr int kBsMode = 0;
@@ -286,7 +294,7 @@ struct Fmt<PULSAR_QUANT_IQ2_XXS> {
     PK_DEV static W load(const uint8_t *row, uint32_t g, uint32_t) {
         const uint8_t *blk = row + (uint64_t)(g >> 2) * kSbBytes;
         W w;
-        w.aux = ld128(blk + 2u + 16u * (g & 3u));
+        w.aux = ldw128(blk + 2u + 16u * (g & 3u));
         w.d = ld16(blk);
         return w;
     }
@@ -357,6 +365,7 @@ PK_DEV int32_t mxfp4_block(uint4 q, uint4 a0, uint4 a1) {
 
 template <>
 struct Fmt<PULSAR_QUANT_MXFP4> {
+    static constexpr bool kHasI1 = false;  // second exact sum (min terms) in use
     static constexpr uint32_t kSbBytes = 136;  // 8 blocks per 256 values
     static constexpr bool kStride32 = false;
     static constexpr int kBsMode = 0;
@@ -369,22 +378,19 @@ struct Fmt<PULSAR_QUANT_MXFP4> {
     PK_DEV static W load(const uint8_t *row, uint32_t g, uint32_t n_blocks) {
         const uint8_t *p = row + 34ull * g;
         W w;
-        w.q0 = ld128(p + 1);
         w.two = 2u * g + 1u < n_blocks ? 1u : 0u;
-        uint32_t e1 = 0;
-        if (w.two) {
-            w.q1 = ld128(p + 18);
-            e1 = p[17];
-        } else {
-            w.q1 = make_uint4(0, 0, 0, 0);
-        }
-        w.e = (uint32_t)p[0] | (e1 << 8);
+        // a unit without a second block (odd block count) re-reads its
+        // first block instead of reading past the row
+        const uint8_t *p1 = w.two ? p + 17 : p;
+        w.q0 = ldw128(p + 1);
+        w.q1 = ldw128(p1 + 1);
+        w.e = (uint32_t)p[0] | ((w.two ? (uint32_t)p1[0] : 0u) << 8);
         return w;
     }
     // sumf += scale_half(e) * sumi for each block with sumi != 0, in block order
     PK_DEV static Part part(const W &w, const Act &a, uint32_t, const uint2 *) {
         const int32_t s0 = mxfp4_block(w.q0, a.q[0], a.q[1]);
-        const int32_t s1 = w.two ? mxfp4_block(w.q1, a.q[2], a.q[3]) : 0;
+        const int32_t s1 = w.two ? mxfp4_block(w.q1, a.q[2], a.q[3]) : 0;  // select, both computed
         float f = 0.0f;
         if (s0 != 0) f += mxfp4_scale_half(w.e & 0xffu) * (float)s0;
         if (s1 != 0) f += mxfp4_scale_half(w.e >> 8) * (float)s1;

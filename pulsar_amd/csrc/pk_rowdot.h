@@ -4,11 +4,11 @@
 // Lane layout: a row is covered by `lpr` lanes (a power of two, >= 4 and
 // >= the unit count, capped at 64), so a wave holds rpp = 64 / lpr rows.
 // Lane `lir` of a row owns units lir, lir + lpr, lir + 2 lpr, ... (UPLMAX
-// at most). The four lanes of a super-block are adjacent, their exact
-// int32 partials meet in a 2-step DPP butterfly, and every lane of the quad
+// at most). The four lanes of a super-block are adjacent; their exact
+// int32 partials meet in the quad's last lane (two DPP row_shr adds), which
 // forms the super-block's fp32 value in the reference's operation order.
-// The quads' values are then summed over the row's lanes in a fixed fp32
-// tree.
+// Those values are then summed into the row group's last lane with DPP
+// row_shr / row_bcast adds, a fixed fp32 tree.
 #pragma once
 
 #include "pk_formats.h"
@@ -21,6 +21,8 @@ struct RowGeom {
     uint32_t lpr_log2;  // lanes per row = 1 << lpr_log2
     uint32_t lir;       // this lane's index within its row group
     uint32_t rip;       // this lane's row within the wave (0 .. rpp-1)
+    // the lane that ends with the row's value (the group's last lane)
+    PK_DEV bool holds_row() const { return lir == (1u << lpr_log2) - 1u; }
 };
 
 // Chooses the lane layout for a row of n_units units.
@@ -34,7 +36,11 @@ static inline uint32_t units_per_row(uint32_t quant, uint32_t in_dim) {
     return 4u * ((in_dim + 255u) / 256u);
 }
 
-PK_DEV RowGeom row_geom(uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2) {
+// L2 > 0 fixes lanes-per-row at compile time (1 << L2); with L2 == 6 a
+// wave holds one row, so row addresses stay wave-uniform (scalar).
+template <uint32_t L2 = 0>
+PK_DEV RowGeom row_geom(uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2_rt) {
+    const uint32_t lpr_log2 = L2 ? L2 : lpr_log2_rt;
     const uint32_t lane = threadIdx.x & 63u;
     RowGeom g;
     g.n_units = n_units;
@@ -63,21 +69,23 @@ PK_DEV void load_row_acts(const pulsar_block_q8_K *xq_row, const RowGeom &rg, Ac
     }
 }
 
-// Loads this lane's weight units of one row.
+// Loads this lane's weight units of one row. Loads are unconditional: a
+// lane whose unit does not exist reads the row's last unit instead (in
+// bounds) and row_partial masks its contribution; callers likewise pass a
+// valid row for rows past the matrix. No predicated loads in the hot loop.
 template <uint32_t Q, uint32_t UPLMAX>
-PK_DEV void load_row_w(const uint8_t *row, bool row_ok, const RowGeom &rg,
-                       typename Fmt<Q>::W (&w)[UPLMAX]) {
+PK_DEV void load_row_w(const uint8_t *row, const RowGeom &rg, typename Fmt<Q>::W (&w)[UPLMAX]) {
 #pragma unroll
     for (uint32_t i = 0; i < UPLMAX; i++) {
         const uint32_t g = rg.lir + (i << rg.lpr_log2);
-        if (row_ok && g < rg.n_units) w[i] = Fmt<Q>::load(row, g, rg.nblk32);
+        if ((i << rg.lpr_log2) >= rg.n_units) continue;  // uniform
+        w[i] = Fmt<Q>::load(row, g < rg.n_units ? g : rg.n_units - 1u, rg.nblk32);
     }
 }
 
-// This lane's share of the row value: every lane of a super-block's quad
-// ends with that super-block's value (the quad's integer sums meet in the
-// butterfly, and each lane forms the same fp32 epilogue from them). All
-// lanes must call it (it exchanges across lanes).
+// This lane's share of the row value: the last lane of each super-block
+// quad holds that super-block's value, every other lane 0. All lanes must
+// call it (it exchanges across lanes).
 template <uint32_t Q, uint32_t UPLMAX>
 PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::W (&w)[UPLMAX],
                          const Act (&a)[UPLMAX], const uint2 *lut) {
@@ -85,25 +93,42 @@ PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::
 #pragma unroll
     for (uint32_t i = 0; i < UPLMAX; i++) {
         const uint32_t g = rg.lir + (i << rg.lpr_log2);
-        if ((i << rg.lpr_log2) >= rg.n_units) break;  // uniform: no unit of this lane set exists
+        if ((i << rg.lpr_log2) >= rg.n_units) continue;  // uniform: no unit of this lane set exists
         const bool ok = row_ok && g < rg.n_units;
         // the super-block exists when its first unit does (a MXFP4 tail
         // super-block may hold fewer than 4 units)
-        const bool sb_ok = row_ok && (g & ~3u) < rg.n_units;
-        Part p = {0, 0, 0.0f};
-        if (ok) p = Fmt<Q>::part(w[i], a[i], g & 3u, lut);
-        p.i0 = group_sum<4>(p.i0);
-        p.i1 = group_sum<4>(p.i1);
-        if (Q == PULSAR_QUANT_MXFP4) p.f = group_sum<4>(p.f);
-        if (sb_ok) acc += Fmt<Q>::sb_value(w[i], a[i].yd, p);
+        const bool sb_ok = row_ok && (g & ~3u) < rg.n_units && (g & 3u) == 3u;
+        // computed on every lane (missing units hold zeroed weights) and
+        // masked afterwards: no divergent branch in the hot loop
+        Part p = Fmt<Q>::part(w[i], a[i], g & 3u, lut);
+        p.i0 = ok ? p.i0 : 0;
+        p.i0 += dpp_shr<1>(p.i0);
+        p.i0 += dpp_shr<2>(p.i0);
+        if (Fmt<Q>::kHasI1) {
+            p.i1 = ok ? p.i1 : 0;
+            p.i1 += dpp_shr<1>(p.i1);
+            p.i1 += dpp_shr<2>(p.i1);
+        }
+        if (Q == PULSAR_QUANT_MXFP4) {
+            p.f = ok ? p.f : 0.0f;
+            p.f += dpp_shr<1>(p.f);
+            p.f += dpp_shr<2>(p.f);
+        }
+        const float v = Fmt<Q>::sb_value(w[i], a[i].yd, p);
+        acc += sb_ok ? v : 0.0f;
     }
     return acc;
 }
 
-// Completes the row value across the row's lanes, starting from quads that
-// each hold one value (result in every lane of the row group).
+// Completes the row value in the row group's last lane (rg.holds_row()),
+// from quads whose last lane holds a value.
 PK_DEV float row_finish(float acc, const RowGeom &rg) {
-    return group_sum_from(acc, 4u, 1u << rg.lpr_log2);
+    const uint32_t l2 = rg.lpr_log2;  // uniform
+    if (l2 >= 3) acc += dpp_shr<4>(acc);
+    if (l2 >= 4) acc += dpp_shr<8>(acc);
+    if (l2 >= 5) acc += dpp_bcast15(acc);
+    if (l2 >= 6) acc += dpp_bcast31(acc);
+    return acc;
 }
 
 }  // namespace pk
