@@ -40,6 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "expert matvec HBM GB/s (% of peak); routed-MoE layer µs/token, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 ROTATE_BYTES = 2_200_000_000
 HEADLINE = "c2_q6k_8192x4096_decode"
 
@@ -128,7 +129,7 @@ def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
     ms = tm["ms"]
     alg = w.nbytes + xq.numel() + out.numel() * 4
     res = {
-        "kernel": "pk::matvec_kernel",
+        "kernel": "pk::mmq_kernel" if (n_tok >= 5 and quant == fm.QUANT_Q6_K) else "pk::matvec_kernel",
         "alg_bytes": alg,
         "us_per_launch": ms * 1e3,
         "us_per_launch_eager": tm["ms_eager"] * 1e3,
@@ -138,6 +139,9 @@ def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
     res["pct_of_peak"] = 100 * res["GBps"] / HBM_PEAK_GBS
     if n_tok > 1:
         res["int_ops"] = 2 * rows * cols * n_tok
+        # int8 MFMA roofline: dense 5.0 POP/s on MI355X
+        res["TOPS"] = res["int_ops"] / (ms * 1e-3) / 1e12
+        res["mfma_frac"] = res["TOPS"] / INT8_PEAK_TOPS
     del copies
     return res
 

@@ -7,7 +7,17 @@
 // bytes of a row, so every wave-wide load is one contiguous span.
 #include "pk_rowdot.h"
 
+// token chunks of at least this many tokens go to the MFMA kernel
+#ifndef PK_MMQ_MIN_TOK
+#define PK_MMQ_MIN_TOK 5u
+#endif
+
 namespace pk {
+
+// mmq.hip: MFMA kernel for token chunks; returns -1 when it has no kernel
+// for the format (the caller then uses the lane kernels)
+int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
+               uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes);
 
 // Each wave streams row passes pass0, pass0 + n_waves, ...: the row's
 // weight units are requested first, then (once per wave) the token's
@@ -224,6 +234,10 @@ extern "C" int pulsar_matmul_kq(void *out, const void *w, const void *xq, uint32
     float *o = (float *)out;
     const uint8_t *wb = (const uint8_t *)w;
     const pulsar_block_q8_K *x = (const pulsar_block_q8_K *)xq;
+    if (n_tok >= PK_MMQ_MIN_TOK) {
+        const int r = pk::launch_mmq(quant, o, wb, x, in_dim, out_dim, n_tok, row_bytes);
+        if (r >= 0) return r;
+    }
     switch (quant) {
     case PULSAR_QUANT_Q4_K: return pk::dispatch_matvec<PULSAR_QUANT_Q4_K>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
     case PULSAR_QUANT_Q6_K: return pk::dispatch_matvec<PULSAR_QUANT_Q6_K>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);

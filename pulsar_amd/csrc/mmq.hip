@@ -1,0 +1,245 @@
+// mmq.hip - dense matvec for token chunks (5..16 tokens per tile) on the
+// int8 matrix cores: v_mfma_i32_16x16x64_i8.
+//
+// A block computes 16 RT weight rows x 16 tokens. Its NW waves split the
+// row's super-blocks (split-K); every wave produces exact int32 group sums
+// with MFMA, applies the format's integer scales in int32, forms the per-
+// super-block fp32 value in the reference's operation order, accumulates its
+// super-blocks in order, and the NW partials are added in wave order through
+// LDS (deterministic).
+//
+// Operand layout of v_mfma_i32_16x16x64_i8 (16 int8 per lane):
+//   A[i][k]: lane i + 16 * kq, K slots of lane group kq
+//   B[k][j]: lane j + 16 * kq, the same K slots
+//   D[i][j]: lane j + 16 * (i / 4), element i % 4
+// Which 16 slots a lane group holds does not matter here: A and B hold the
+// same ones, and every sum below is over whole lane groups.
+#include "pk_rowdot.h"
+
+namespace pk {
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+
+PK_DEV v4i mfma16x16x32(uint2 a, uint2 b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), z, 0,
+                                                 0, 0);
+}
+
+// LDS loads at aligned offsets
+PK_DEV uint2 lds64(const uint8_t *p) { return *(const uint2 *)p; }
+PK_DEV uint4 lds128(const uint8_t *p) { return *(const uint4 *)p; }
+PK_DEV float4 lds_f4(const float *p) { return *(const float4 *)p; }
+
+// ----------------------------------------------------------------- Q6_K --
+// Step s = (h, q) of a super-block covers values 128h + 32q + [0, 32):
+// group g0 = 8h + 2q (values 0..15: lane groups kq 0, 1) and g0 + 1 (lane
+// groups 2, 3). Lane group kq holds values 8kq .. 8kq+7 of the step, for A
+// (the tokens' q8 bytes 128h + 32q + 8kq) and B (the rows' codes: nibble
+// q / 2 of ql[64h + 32 (q & 1) + 8kq], bits 2q..2q+1 of qh[32h + 8kq]).
+// MFMA(A, B) sums both groups, MFMA(A, B with lane groups 2, 3 zeroed) the
+// first, so sc0 D0 + sc1 D1 = (sc0 - sc1) D_lo + sc1 D_all, exact in int32.
+struct MmaQ6K {
+    static constexpr uint32_t kSbBytes = 210;
+    static constexpr uint32_t kDOff = 208;  // f16 d within the block
+    struct W {
+        uint2 la[2], lb[2], qh[2];
+        uint4 sc;
+        uint32_t d;
+    };
+    // from an LDS copy of the super-block (8-byte aligned)
+    PK_DEV static W load_lds(const uint8_t *blk, uint32_t kq, uint32_t d_off) {
+        W w;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            w.la[h] = lds64(blk + 64 * h + 8 * kq);
+            w.lb[h] = lds64(blk + 64 * h + 32 + 8 * kq);
+            w.qh[h] = lds64(blk + 128 + 32 * h + 8 * kq);
+        }
+        w.sc = lds128(blk + 192);
+        w.d = *(const uint16_t *)(blk + d_off);
+        return w;
+    }
+    // signed code c - 32 of four values: the low nibble, plus the 2 high
+    // bits h mapped through the byte table {0xE0, 0xF0, 0x00, 0x10} =
+    // (h - 2) << 4 (v_perm_b32 picks table byte h for every byte)
+    PK_DEV static uint32_t code(uint32_t l, uint32_t qh, uint32_t nsh, uint32_t hsh) {
+        const uint32_t hf = (qh >> hsh) & 0x03030303u;
+        const uint32_t hi = __builtin_amdgcn_perm(0u, 0x1000F0E0u, hf);
+        return ((l >> nsh) & 0x0f0f0f0fu) | hi;
+    }
+    // B operand of step (h, q)
+    PK_DEV static uint2 codes(const W &w, int h, int q) {
+        const uint2 l = (q & 1) ? w.lb[h] : w.la[h];
+        const uint32_t nsh = (q >> 1) ? 4u : 0u, hsh = 2u * q;
+        return make_uint2(code(l.x, w.qh[h].x, nsh, hsh), code(l.y, w.qh[h].y, nsh, hsh));
+    }
+};
+
+#ifndef PK_MMQ_RT
+#define PK_MMQ_RT 2u
+#endif
+#ifndef PK_MMQ_C
+#define PK_MMQ_C 4u
+#endif
+
+// Tile of 16 RT rows x 16 tokens, K walked in chunks of C super-blocks.
+// Each chunk's weights (16 RT rows x C super-blocks) and activations (16
+// tokens x C super-blocks) are copied HBM -> LDS with row-contiguous
+// 16-byte loads (a wave's load covers 4 consecutive super-blocks of one
+// row), the next chunk's loads are issued before the current chunk's MFMAs,
+// and wave (rt, sb) = (w / C, w % C) takes row tile rt, super-block sb of
+// each chunk. LDS rows are padded so the 16 rows (tokens) an MFMA operand
+// read touches fall in distinct banks.
+template <uint32_t Q, uint32_t RT, uint32_t C>
+struct MmqTile {
+    static constexpr uint32_t NW = RT * C;                          // waves
+    static constexpr uint32_t NT = 64u * NW;                        // threads
+    static constexpr uint32_t kRows = 16u * RT;
+    static constexpr uint32_t kSb = MmaQ6K::kSbBytes;               // bytes per row super-block
+    static constexpr uint32_t kChunks = (kSb + 15u) / 16u;          // 16-byte loads per row super-block
+    static constexpr uint32_t kSlot = 16u * kChunks;                // LDS bytes per row super-block
+    // the last load of a super-block reads its final 16 bytes (kSb - 16 ..)
+    // and is stored at slot offset 16 (kChunks - 1): d lands here
+    static constexpr uint32_t kDSlot = 16u * (kChunks - 1u) + MmaQ6K::kDOff - (kSb - 16u);
+    static constexpr uint32_t kRowPitch = C * kSlot + 16u;          // LDS bytes per row (padded)
+    static constexpr uint32_t kActPitch = 256u + 16u;               // LDS bytes per (token, super-block)
+    static constexpr uint32_t kWLoads = kRows * C * 16u / NT;       // weight loads per thread
+    static constexpr uint32_t kALoads = 16u * C * 16u / NT;         // activation loads per thread
+    static_assert(kRows * C * 16u % NT == 0 && 16u * C * 16u % NT == 0, "tile shape");
+    static_assert(C * 16u <= NT, "one activation scale per thread");
+};
+
+template <uint32_t Q, uint32_t RT, uint32_t C>
+__global__ __launch_bounds__(64 * RT * C) void mmq_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
+                                                          const pulsar_block_q8_K *__restrict__ xq, uint32_t nb,
+                                                          uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
+    using T = MmqTile<Q, RT, C>;
+    __shared__ __align__(16) uint8_t wl[T::kRows * T::kRowPitch];
+    __shared__ __align__(16) uint8_t al[C * 16u * T::kActPitch];
+    __shared__ __align__(16) float yl[C * 16u];
+    __shared__ float part[T::NW][16][17];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t i = lane & 15u, kq = lane >> 4;
+    const uint32_t r0 = blockIdx.x * T::kRows, t0 = blockIdx.y * 16u;
+    const uint8_t *xb = (const uint8_t *)xq;
+    const uint64_t tok_bytes = (uint64_t)nb * 292u;
+
+    // ---- HBM -> registers -> LDS copy of one chunk (super-blocks kb ..).
+    // Per-thread source pointers (chunk 0) and LDS offsets are fixed.
+    const uint8_t *wsrc[T::kWLoads];
+    uint32_t wsb[T::kWLoads], wdst[T::kWLoads];
+    bool wact[T::kWLoads];
+#pragma unroll
+    for (uint32_t m = 0; m < T::kWLoads; m++) {
+        const uint32_t f = tid + T::NT * m, c = f & 15u, rs = f >> 4;
+        const uint32_t row = rs / C, sb = rs % C;
+        const uint32_t gr = r0 + row < out_dim ? r0 + row : out_dim - 1u;
+        const uint32_t off = 16u * c < T::kSb - 16u ? 16u * c : T::kSb - 16u;
+        wsrc[m] = w + (uint64_t)gr * row_bytes + (uint64_t)sb * T::kSb + off;
+        wsb[m] = sb;
+        wdst[m] = row * T::kRowPitch + sb * T::kSlot + 16u * c;
+        wact[m] = c < T::kChunks;
+    }
+    const uint8_t *asrc[T::kALoads];
+    uint32_t asb[T::kALoads], adst[T::kALoads];
+#pragma unroll
+    for (uint32_t m = 0; m < T::kALoads; m++) {
+        const uint32_t f = tid + T::NT * m, c = f & 15u, ts = f >> 4;
+        const uint32_t t = ts / C, sb = ts % C;
+        const uint32_t gt = t0 + t < n_tok ? t0 + t : n_tok - 1u;
+        asrc[m] = xb + gt * tok_bytes + (uint64_t)sb * 292u + 4u + 16u * c;
+        asb[m] = sb;
+        adst[m] = (sb * 16u + t) * T::kActPitch + 16u * c;
+    }
+    const uint32_t ysb = tid % C, yt = tid / C;
+    const uint8_t *ysrc = xb + (t0 + yt < n_tok ? t0 + yt : n_tok - 1u) * tok_bytes + (uint64_t)ysb * 292u;
+    const bool yact = tid < C * 16u;
+
+    uint4 wreg[T::kWLoads], areg[T::kALoads];
+    uint32_t yreg = 0;
+    auto gload = [&](uint32_t kb) {
+#pragma unroll
+        for (uint32_t m = 0; m < T::kWLoads; m++)
+            if (wact[m] && kb + wsb[m] < nb) wreg[m] = ld128(wsrc[m] + (uint64_t)kb * T::kSb);
+#pragma unroll
+        for (uint32_t m = 0; m < T::kALoads; m++)
+            if (kb + asb[m] < nb) areg[m] = ld128(asrc[m] + (uint64_t)kb * 292u);
+        if (yact && kb + ysb < nb) yreg = ld32(ysrc + (uint64_t)kb * 292u);
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (uint32_t m = 0; m < T::kWLoads; m++)
+            if (wact[m]) *(uint4 *)(wl + wdst[m]) = wreg[m];
+#pragma unroll
+        for (uint32_t m = 0; m < T::kALoads; m++) *(uint4 *)(al + adst[m]) = areg[m];
+        if (yact) yl[ysb * 16u + yt] = __builtin_bit_cast(float, yreg);
+    };
+
+    const uint32_t rt = wave / C, sbw = wave % C;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    gload(0);
+    for (uint32_t kb = 0; kb < nb; kb += C) {
+        lstore();
+        __syncthreads();
+        if (kb + C < nb) gload(kb + C);  // in flight during this chunk's MFMAs
+        if (kb + sbw < nb) {
+            uint2 a[8];
+            const uint8_t *ab = al + (sbw * 16u + i) * T::kActPitch + 8u * kq;
+#pragma unroll
+            for (int st = 0; st < 8; st++) a[st] = lds64(ab + 32u * st);
+            const float4 yd4 = lds_f4(yl + sbw * 16u + 4u * kq);
+            const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
+            const MmaQ6K::W wv =
+                MmaQ6K::load_lds(wl + (rt * 16u + i) * T::kRowPitch + sbw * T::kSlot, kq, T::kDSlot);
+            int32_t isum[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                const int h = st >> 2, q = st & 3;
+                const uint2 c = MmaQ6K::codes(wv, h, q);
+                const uint2 c_lo = kq < 2 ? c : make_uint2(0u, 0u);
+                const v4i d_all = mfma16x16x32(a[st], c);
+                const v4i d_lo = mfma16x16x32(a[st], c_lo);
+                const int32_t s0 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q);
+                const int32_t s1 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q + 1);
+#pragma unroll
+                // |d| < 2^17, |s| < 2^8: 24-bit multiplies are exact
+                for (int r = 0; r < 4; r++) isum[r] += __mul24(s0 - s1, d_lo[r]) + __mul24(s1, d_all[r]);
+            }
+            const float xd = f16f((uint16_t)wv.d);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] += xd * yd[r] * (float)isum[r];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) part[wave][i][4 * kq + r] = acc[r];
+    __syncthreads();
+    for (uint32_t e = tid; e < 16u * T::kRows; e += T::NT) {
+        const uint32_t row = e % T::kRows, tok = e / T::kRows;
+        if (r0 + row < out_dim && t0 + tok < n_tok) {
+            const uint32_t prt = row / 16u;
+            float v = part[prt * C][row % 16u][tok];
+#pragma unroll
+            for (uint32_t k = 1; k < C; k++) v += part[prt * C + k][row % 16u][tok];
+            out[(uint64_t)(t0 + tok) * out_dim + r0 + row] = v;
+        }
+    }
+}
+
+int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
+               uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
+    constexpr uint32_t RT = PK_MMQ_RT, C = PK_MMQ_C;
+    const uint32_t nb = in_dim / 256u;
+    const dim3 grid((out_dim + 16u * RT - 1u) / (16u * RT), (n_tok + 15u) / 16u);
+    switch (quant) {
+    case PULSAR_QUANT_Q6_K:
+        hipLaunchKernelGGL((mmq_kernel<PULSAR_QUANT_Q6_K, RT, C>), grid, dim3(64 * RT * C), 0, pk::stream(), out,
+                           w, xq, nb, out_dim, n_tok, row_bytes);
+        return launch_ok("matmul_kq mmq launch");
+    default:
+        return -1;  // no MFMA kernel for this format: caller falls back
+    }
+}
+
+}  // namespace pk

@@ -74,7 +74,8 @@ def unit_scale_matrix(quant, rows, n, seed):
 
 
 @pytest.mark.parametrize("quant", DENSE)
-@pytest.mark.parametrize("n,rows,n_tok", [(256, 37, 1), (2048, 64, 1), (4096, 33, 3), (12288, 9, 1)])
+@pytest.mark.parametrize("n,rows,n_tok", [(256, 37, 1), (2048, 64, 1), (4096, 33, 3), (12288, 9, 1),
+                                          (256, 21, 7), (4096, 37, 16), (2048, 50, 20), (1024, 16, 5)])
 def test_matvec_integer_stage_exact(dev, quant, n, rows, n_tok):
     w = unit_scale_matrix(quant, rows, n, n + rows)
     xq = unit_scale_xq(n_tok, n)
@@ -89,7 +90,8 @@ def test_matvec_integer_stage_exact(dev, quant, n, rows, n_tok):
 
 @pytest.mark.parametrize("quant", DENSE)
 @pytest.mark.parametrize("n,rows,n_tok", [(256, 5, 1), (2048, 130, 1), (4096, 77, 2), (4096, 40, 5),
-                                          (4096, 24, 16), (8192, 19, 1), (20480, 7, 1)])
+                                          (4096, 24, 16), (8192, 19, 1), (20480, 7, 1),
+                                          (2816, 33, 9), (4096, 70, 33)])
 def test_matvec_fp32_parity(dev, quant, n, rows, n_tok):
     w = synth.quant_matrix(quant, rows, n, synth.rng_for(n * rows + n_tok, "mv"))
     x = rng.standard_normal((n_tok, n)).astype(np.float32)
@@ -103,19 +105,22 @@ def test_matvec_fp32_parity(dev, quant, n, rows, n_tok):
         assert_rows_close(got[t], np.array(vals, np.float32), np.array(scale), f"q{quant} n{n} t{t}")
 
 
-def test_matvec_padded_row_stride(dev):
+@pytest.mark.parametrize("n_tok", [1, 16])
+def test_matvec_padded_row_stride(dev, n_tok):
     # row_bytes larger than the packed row: rows start row_bytes apart
+    # (n_tok 16 runs the MFMA kernel)
     n, rows, quant = 1024, 21, QUANT_Q6_K
     rb = row_bytes(quant, n)
     w = synth.quant_matrix(quant, rows, n, synth.rng_for(5, "pad"))
     padded = np.zeros((rows, rb + 46), np.uint8)
     padded[:, :rb] = w
-    xq = oracle.quantize_q8_k(rng.standard_normal((1, n)).astype(np.float32))
-    out = zeros_f32((1, rows))
-    K.matmul_kq(out, up(padded), up(xq), n, rows, 1, rb + 46, quant)
-    want = oracle.matmul_kq(padded, xq, n, rows, 1, rb + 46, quant)
-    vals, scale = zip(*(oracle.vec_dot(quant, w[r], xq[0], n) for r in range(rows)))
-    assert_rows_close(down(out)[0], want[0], np.array(scale), "padded stride")
+    xq = oracle.quantize_q8_k(rng.standard_normal((n_tok, n)).astype(np.float32))
+    out = zeros_f32((n_tok, rows))
+    K.matmul_kq(out, up(padded), up(xq), n, rows, n_tok, rb + 46, quant)
+    want = oracle.matmul_kq(padded, xq, n, rows, n_tok, rb + 46, quant)
+    for t in range(n_tok):
+        vals, scale = zip(*(oracle.vec_dot(quant, w[r], xq[t], n) for r in range(rows)))
+        assert_rows_close(down(out)[t], want[t], np.array(scale), f"padded stride t{t}")
 
 
 def test_matvec_linearity_exact(dev):
