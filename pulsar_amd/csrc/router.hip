@@ -8,29 +8,45 @@ namespace pk {
 // stride the row with 16-byte loads; every token of the batch reuses the
 // row from registers/L1 (pulsar_kernels.cu:6504-6524 computes the same
 // sums, block-per-(row, token)).
-__global__ __launch_bounds__(64) void matmul_f32_kernel(float *__restrict__ out,
-                                                        const float *__restrict__ w,
-                                                        const float *__restrict__ x,
-                                                        uint32_t in_dim, uint32_t out_dim,
-                                                        uint32_t n_tok) {
-    const uint32_t row = blockIdx.x;
-    const uint32_t lane = threadIdx.x;
+// One wave per (row, group of TG tokens): lanes stride over K with 16-byte
+// loads of the row and of the TG token vectors, then a wave reduction per
+// token. Waves of a block take consecutive rows of the same token group, so
+// the token vectors are shared through the cache.
+template <uint32_t TG>
+__global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out, const float *__restrict__ w,
+                                                         const float *__restrict__ x, uint32_t in_dim,
+                                                         uint32_t out_dim, uint32_t n_tok, uint32_t n_work) {
+    const uint32_t gw = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    if (gw >= n_work) return;  // wave-uniform
+    const uint32_t row = gw % out_dim, t0 = (gw / out_dim) * TG;
     const float *wr = w + (uint64_t)row * in_dim;
+    const float *xr[TG];
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) xr[t] = x + (uint64_t)(t0 + t < n_tok ? t0 + t : n_tok - 1u) * in_dim;
+    float acc[TG];
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) acc[t] = 0.0f;
     const uint32_t n4 = in_dim / 4u;
-    for (uint32_t t = 0; t < n_tok; t++) {
-        const float *xr = x + (uint64_t)t * in_dim;
-        float acc = 0.0f;
-        for (uint32_t i = lane; i < n4; i += 64u) {
-            const uint4 a = ld128((const uint8_t *)(wr + 4u * i));
-            const uint4 b = ld128((const uint8_t *)(xr + 4u * i));
-            acc += __uint_as_float(a.x) * __uint_as_float(b.x);
-            acc += __uint_as_float(a.y) * __uint_as_float(b.y);
-            acc += __uint_as_float(a.z) * __uint_as_float(b.z);
-            acc += __uint_as_float(a.w) * __uint_as_float(b.w);
+    for (uint32_t i = lane; i < n4; i += 64u) {
+        const uint4 a = ld128((const uint8_t *)(wr + 4u * i));
+#pragma unroll
+        for (uint32_t t = 0; t < TG; t++) {
+            const uint4 b = ld128((const uint8_t *)(xr[t] + 4u * i));
+            acc[t] += __uint_as_float(a.x) * __uint_as_float(b.x);
+            acc[t] += __uint_as_float(a.y) * __uint_as_float(b.y);
+            acc[t] += __uint_as_float(a.z) * __uint_as_float(b.z);
+            acc[t] += __uint_as_float(a.w) * __uint_as_float(b.w);
         }
-        for (uint32_t i = 4u * n4 + lane; i < in_dim; i += 64u) acc += wr[i] * xr[i];
-        acc = group_sum<64>(acc);
-        if (lane == 0) out[(uint64_t)t * out_dim + row] = acc;
+    }
+    for (uint32_t i = 4u * n4 + lane; i < in_dim; i += 64u) {
+#pragma unroll
+        for (uint32_t t = 0; t < TG; t++) acc[t] += wr[i] * xr[t][i];
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) {
+        const float v = group_sum<64>(acc[t]);
+        if (lane == 0 && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = v;
     }
 }
 
@@ -53,16 +69,35 @@ PK_DEV float router_sigmoid(float x) {
     return e / (1.0f + e);
 }
 
-// higher score wins; ties go to the lower expert index (pulsar_kernels.cu:922-925)
-PK_DEV bool better(float av, uint32_t ai, float bv, uint32_t bi) {
-    return av > bv || (av == bv && ai < bi);
-}
-
 constexpr uint32_t kMaxPerLane = 16;  // 64 lanes x 16 = 1024 routed logits
 
-// One wave per token (pulsar_kernels.cu:938-1050 semantics): k rounds of a
-// wave-wide arg-max over (score, index); lane 0 then normalises the k
-// winners' weights in selection order.
+// Order-preserving key of a routing score: larger score <=> larger key,
+// -0 and +0 equal, every non-NaN score >= 1 and NaN 0. The reference's
+// comparator (pulsar_kernels.cu:922-925) lets the higher score win, ties
+// going to the lower expert index, and never picks a NaN.
+PK_DEV uint32_t score_key(float v) {
+    if (v != v) return 0u;
+    const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);  // -0 -> +0
+    return ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) + 1u;
+}
+
+PK_DEV uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (uint32_t s = 1; s < 64u; s <<= 1) {
+        const uint32_t o = (uint32_t)partner((int32_t)v, s);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// One wave per token (pulsar_kernels.cu:938-1050 semantics). Lane l holds
+// experts lJ .. lJ+J-1, so a lower lane means a lower expert index. Each of
+// the k rounds takes the wave maximum of the lanes' best keys; the lowest
+// lane holding it owns the winner (highest score, lowest index on ties),
+// which it replaces by -inf like the reference, so an expert can win again
+// once every remaining score is -inf. Weights are then normalised per the
+// softmax mode, with the reference's sequential sums.
+template <uint32_t J>
 __global__ __launch_bounds__(64) void router_select_kernel(int32_t *__restrict__ selected,
                                                            float *__restrict__ weights,
                                                            const float *__restrict__ logits,
@@ -70,95 +105,108 @@ __global__ __launch_bounds__(64) void router_select_kernel(int32_t *__restrict__
                                                            uint32_t n_expert, uint32_t k_used,
                                                            float weight_scale, uint32_t mode,
                                                            uint32_t n_shexp) {
+    __shared__ int32_t sel_l[64u * kMaxPerLane + 64u];
+    __shared__ float w_l[64u * kMaxPerLane + 64u];
+    __shared__ float es_l;
     const uint32_t token = blockIdx.x;
     const uint32_t lane = threadIdx.x;
     const uint32_t sink = mode == 2u ? n_shexp : 0u;
     const uint32_t n_logit = n_expert + sink;
     const uint32_t n_slot = k_used + sink;
     const float *lg = logits + (uint64_t)token * n_logit;
-    int32_t *sel = selected + (uint64_t)token * n_slot;
-    float *w = weights + (uint64_t)token * n_slot;
 
-    float prob[kMaxPerLane], score[kMaxPerLane];
+    const uint32_t kNegInf = score_key(-INFINITY);
+    uint32_t key[J];
+    float prob[J];
 #pragma unroll
-    for (uint32_t j = 0; j < kMaxPerLane; j++) {
-        const uint32_t e = lane + 64u * j;
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane * J + j;
         if (e < n_expert) {
             const float raw = lg[e];
             const float p = mode == 1u ? raw : router_sigmoid(raw);
             prob[j] = mode == 2u ? raw : p;  // mode 2 weights use the raw winner logit
-            score[j] = p + (bias ? bias[e] : 0.0f);
+            key[j] = score_key(p + (bias ? bias[e] : 0.0f));
         } else {
             prob[j] = 0.0f;
-            score[j] = -INFINITY;
+            key[j] = 0u;
         }
     }
-    for (uint32_t k = 0; k < k_used; k++) {
-        float bs = -INFINITY, bp = 0.0f;
-        uint32_t bi = UINT32_MAX;
+    // this lane's best: first (lowest index) maximal key
+    uint32_t bk = 0u, bj = 0u;
+    float bp = 0.0f;
+    auto lane_best = [&]() {
+        bk = 0u;
+        bj = 0u;
+        bp = 0.0f;
 #pragma unroll
-        for (uint32_t j = 0; j < kMaxPerLane; j++) {
-            const uint32_t e = lane + 64u * j;
-            if (e < n_expert && better(score[j], e, bs, bi)) {
-                bs = score[j];
+        for (uint32_t j = 0; j < J; j++)
+            if (key[j] > bk) {
+                bk = key[j];
+                bj = j;
                 bp = prob[j];
-                bi = e;
+            }
+    };
+    lane_best();
+    float sum = 0.0f, wmax = -INFINITY;
+    for (uint32_t k = 0; k < k_used; k++) {
+        const uint32_t m = wave_max_u32(bk);
+        int32_t win = -1;  // no candidate: every routed score is NaN
+        float wp = 0.0f;
+        if (m != 0u) {
+            const uint64_t bal = __ballot(bk == m);
+            const int f = __builtin_ctzll(bal);
+            win = __builtin_amdgcn_readlane((int)(lane * J + bj), f);
+            wp = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bp), f));
+            if ((int)lane == f) {
+#pragma unroll
+                for (uint32_t j = 0; j < J; j++)
+                    if (j == bj) key[j] = kNegInf;
+                lane_best();
             }
         }
-#pragma unroll
-        for (uint32_t m = 1; m < 64u; m <<= 1) {
-            const float os = lane_xor(bs, m);
-            const float op = lane_xor(bp, m);
-            const uint32_t oi = (uint32_t)lane_xor((int32_t)bi, m);
-            if (better(os, oi, bs, bi)) {
-                bs = os;
-                bp = op;
-                bi = oi;
-            }
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < kMaxPerLane; j++)
-            if (lane + 64u * j == bi) score[j] = -INFINITY;
         if (lane == 0) {
-            sel[k] = (int32_t)bi;
-            w[k] = bp;
+            sel_l[k] = win;
+            w_l[k] = wp;
         }
+        sum += wp;
+        wmax = fmaxf(wmax, wp);
     }
-    if (lane != 0) return;
-    if (mode == 2u) {
-        // shared "sink" experts appended as always-on slots; weights are
-        // softmax(logsigmoid(raw)) * scale over winners ++ sinks
-        for (uint32_t s = 0; s < sink; s++) {
-            sel[k_used + s] = (int32_t)(n_expert + s);
-            w[k_used + s] = lg[n_expert + s];
-        }
-        float m = -INFINITY;
-        for (uint32_t k = 0; k < n_slot; k++) {
-            const float x = w[k];
-            w[k] = x < 0.0f ? x - log1pf(expf(x)) : -log1pf(expf(-x));
-            m = fmaxf(m, w[k]);
-        }
-        float es = 0.0f;
-        for (uint32_t k = 0; k < n_slot; k++) {
-            w[k] = expf(w[k] - m);
-            es += w[k];
-        }
-        for (uint32_t k = 0; k < n_slot; k++) w[k] = w[k] / es * weight_scale;
-    } else if (mode == 1u) {
-        // softmax -> top-k -> renormalise == softmax over the k winners
-        float m = -INFINITY;
-        for (uint32_t k = 0; k < k_used; k++) m = fmaxf(m, w[k]);
-        float es = 0.0f;
-        for (uint32_t k = 0; k < k_used; k++) {
-            w[k] = expf(w[k] - m);
-            es += w[k];
-        }
-        for (uint32_t k = 0; k < k_used; k++) w[k] = w[k] / es * weight_scale;
-    } else {
-        float sum = 0.0f;
-        for (uint32_t k = 0; k < k_used; k++) sum += w[k];
+    // mode 2: shared "sink" experts appended as always-on slots
+    for (uint32_t sh = lane; sh < sink; sh += 64u) {
+        sel_l[k_used + sh] = (int32_t)(n_expert + sh);
+        w_l[k_used + sh] = lg[n_expert + sh];
+    }
+    __syncthreads();
+    if (mode == 0u) {
         sum = fmaxf(sum, 6.103515625e-5f);
-        for (uint32_t k = 0; k < k_used; k++) w[k] = w[k] / sum * weight_scale;
+    } else {
+        // mode 1: softmax over the k winners (== softmax -> top-k ->
+        // renormalise); mode 2: softmax(logsigmoid(raw)) over winners ++ sinks
+        float m = mode == 1u ? wmax : -INFINITY;
+        for (uint32_t p = lane; p < n_slot; p += 64u) {
+            float x = w_l[p];
+            if (mode == 2u) {
+                x = x < 0.0f ? x - log1pf(expf(x)) : -log1pf(expf(-x));
+                m = fmaxf(m, x);
+            }
+            w_l[p] = x;
+        }
+        if (mode == 2u) m = wave_max(m);
+        for (uint32_t p = lane; p < n_slot; p += 64u) w_l[p] = expf(w_l[p] - m);
+        __syncthreads();
+        if (lane == 0) {
+            float es = 0.0f;
+            for (uint32_t p = 0; p < n_slot; p++) es += w_l[p];
+            es_l = es;
+        }
+        __syncthreads();
+        sum = es_l;
+    }
+    int32_t *sel = selected + (uint64_t)token * n_slot;
+    float *w = weights + (uint64_t)token * n_slot;
+    for (uint32_t p = lane; p < n_slot; p += 64u) {
+        sel[p] = sel_l[p];
+        w[p] = w_l[p] / sum * weight_scale;
     }
 }
 
@@ -167,8 +215,17 @@ __global__ __launch_bounds__(64) void router_select_kernel(int32_t *__restrict__
 extern "C" int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32_t in_dim,
                                  uint32_t out_dim, uint32_t n_tok) {
     if (!out || !w || !x || in_dim == 0 || out_dim == 0 || n_tok == 0) return pk::reject("matmul f32");
-    hipLaunchKernelGGL(pk::matmul_f32_kernel, dim3(out_dim), dim3(64), 0, pk::stream(), (float *)out,
-                       (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
+    // tokens in groups of 4 (1 for a single token); one wave per (row, group)
+    const uint32_t tg = n_tok == 1u ? 1u : 4u;
+    const uint64_t work = (uint64_t)out_dim * ((n_tok + tg - 1u) / tg);
+    if (work > 0xffffffffull - 3u) return pk::reject("matmul f32 (size)");
+    const dim3 grid((uint32_t)((work + 3u) / 4u));
+    if (tg == 1u)
+        hipLaunchKernelGGL(pk::matmul_f32_kernel<1>, grid, dim3(256), 0, pk::stream(), (float *)out,
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, (uint32_t)work);
+    else
+        hipLaunchKernelGGL(pk::matmul_f32_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)out,
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, (uint32_t)work);
     return pk::launch_ok("matmul f32 launch");
 }
 
@@ -189,8 +246,16 @@ extern "C" int pulsar_router_select(void *selected, void *weights, const void *l
         n_tok == 0 || softmax_mode > 2u || (softmax_mode != 2u && n_shexp != 0) ||
         n_expert + (softmax_mode == 2u ? n_shexp : 0u) > 1024u || n_expert > 64u * pk::kMaxPerLane)
         return pk::reject("router select");
-    hipLaunchKernelGGL(pk::router_select_kernel, dim3(n_tok), dim3(64), 0, pk::stream(), (int32_t *)selected,
-                       (float *)weights, (const float *)logits, (const float *)bias, n_expert, k_used,
-                       weight_scale, softmax_mode, n_shexp);
+#define PK_SELECT(J)                                                                                        \
+    hipLaunchKernelGGL(pk::router_select_kernel<J>, dim3(n_tok), dim3(64), 0, pk::stream(), (int32_t *)selected, \
+                       (float *)weights, (const float *)logits, (const float *)bias, n_expert, k_used,           \
+                       weight_scale, softmax_mode, n_shexp)
+    if (n_expert <= 256u)
+        PK_SELECT(4);
+    else if (n_expert <= 512u)
+        PK_SELECT(8);
+    else
+        PK_SELECT(16);
+#undef PK_SELECT
     return pk::launch_ok("router select launch");
 }

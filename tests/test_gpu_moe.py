@@ -211,6 +211,31 @@ def test_router_select(dev, n_expert, k, n_tok, mode):
     assert np.allclose(down(w), want_w, rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_router_select_ties_inf_nan(dev, mode):
+    """Tied scores go to the lower index; -inf and NaN logits: NaN never
+    wins, and once only -inf remain the lowest index wins again (the
+    reference's removed experts are set to -inf, not dropped)."""
+    n_expert, k, n_tok = 300, 12, 4
+    logits = np.full((n_tok, n_expert), 0.5, np.float32)   # all tied
+    logits[1, ::7] = -np.inf
+    logits[1, 3:5] = 2.0
+    logits[2, :] = -np.inf
+    logits[2, 10:13] = 1.0                                  # 3 finite, k = 12
+    logits[3, ::3] = np.nan
+    logits[3, 100] = 3.0
+    bias = np.zeros(n_expert, np.float32)
+    sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
+    w = zeros_f32((n_tok, k))
+    K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.0, n_tok, mode, 0)
+    want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.0, n_tok, mode, 0)
+    assert np.array_equal(down(sel), want_sel)
+    got_w = down(w)
+    assert np.array_equal(np.isnan(got_w), np.isnan(want_w))
+    ok = ~np.isnan(want_w)
+    assert np.allclose(got_w[ok], want_w[ok], rtol=0, atol=1e-6)
+
+
 def test_matmul_f32_and_bias(dev):
     for in_dim, out_dim, n_tok in ((2048, 256, 1), (4096, 128, 16), (2880, 32, 64), (37, 5, 3)):
         wt = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float32)
