@@ -53,6 +53,8 @@ def parse_args():
     ap.add_argument("--only", nargs="*", default=None, help="subset of result names")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="only the workload of the rocprofv3 --pmc traffic passes (no timing, no JSON)")
     return ap.parse_args()
 
 
@@ -294,17 +296,30 @@ def cpu_baseline(seconds: float) -> dict:
     x = synth.activations(1, cols, synth.rng_for(12, HEADLINE))
     xq = oracle.quantize_q8_k(x)
     out = np.zeros((1, rows), np.float32)
+    # this process's CPU share (16 threads on the GPU boxes, whatever nproc says)
     avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     threads = max(1, min(16, avail))
+    lane_threads = max(1, threads // 2 - 2)  # the lane's default pool, (logical / 2) - 2 (elib:1896)
     rb = row_bytes(QUANT_Q6_K, cols)
-    oracle.matmul_kq_mt(copies[0], xq, cols, rows, 1, rb, QUANT_Q6_K, threads, out)  # warm the pool
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < seconds:
-        oracle.matmul_kq_mt(copies[n % n_copies], xq, cols, rows, 1, rb, QUANT_Q6_K, threads, out)
-        n += 1
-    dt = time.perf_counter() - t0
     alg = w.nbytes + xq.nbytes + out.nbytes
+
+    def timed(nt, budget):
+        oracle.matmul_kq_mt(copies[0], xq, cols, rows, 1, rb, QUANT_Q6_K, nt, out)  # warm the pool
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < budget:
+            oracle.matmul_kq_mt(copies[n % n_copies], xq, cols, rows, 1, rb, QUANT_Q6_K, nt, out)
+            n += 1
+        return n, time.perf_counter() - t0
+
+    n, dt = timed(threads, seconds * 0.6)
+    n_l, dt_l = timed(lane_threads, seconds * 0.4)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     return {
         "value": alg * n / dt / 1e9,
         "unit": "GB/s",
@@ -313,7 +328,39 @@ def cpu_baseline(seconds: float) -> dict:
         "sample": f"{n} passes of the Q6_K 8192x4096 decode matvec in {dt:.1f} s, {threads} threads, "
                   f"{n_copies} rotating host copies ({n_copies * w.nbytes / 1e9:.1f} GB)",
         "us_per_pass": dt / n * 1e6,
+        "lane_default": {"threads": lane_threads, "value": alg * n_l / dt_l / 1e9, "unit": "GB/s",
+                         "us_per_pass": dt_l / n_l * 1e6},
+        "cpu_model": model,
+        "logical_cpus_visible": os.cpu_count(),
     }
+
+
+def pmc_run(ctx):
+    """Workload of the `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
+    passes: 20 eager launches each of the c2 decode matvec and the c2
+    16-token MFMA matvec over rotating weight copies, then five copies of a
+    256 MiB device buffer (reads 256 MiB, writes 256 MiB: the calibration of
+    both counters)."""
+    torch, K, synth, fm = ctx["torch"], ctx["K"], ctx["synth"], ctx["fm"]
+    q, rows, cols = fm.QUANT_Q6_K, 8192, 4096
+    w = synth.quant_matrix(q, rows, cols, synth.rng_for(11, "pmc"))
+    copies = dev_copies(torch, w, 1_000_000_000)
+    rb = fm.row_bytes(q, cols)
+    for n_tok in (1, 16):
+        x = torch.from_numpy(synth.activations(n_tok, cols, synth.rng_for(12, "pmc"))).cuda()
+        xq = torch.zeros(n_tok * fm.q8k_blocks(cols) * 292, dtype=torch.uint8, device="cuda")
+        K.quantize_q8_k(xq, x, cols, n_tok)
+        out = torch.zeros((n_tok, rows), dtype=torch.float32, device="cuda")
+        for i in range(20):
+            K.matmul_kq(out, copies[i % copies.shape[0]], xq, cols, rows, n_tok, rb, q)
+        torch.cuda.synchronize()
+    del copies
+    src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc-run done", flush=True)
 
 
 def pmc_traffic(name: str):
@@ -342,6 +389,9 @@ def main():
     _lib.load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     ctx = {"torch": torch, "K": K, "synth": synth, "fm": fm, "timer": Timer(torch, K)}
+    if args.pmc_run:
+        pmc_run(ctx)
+        return
     steps, warmup = args.steps, args.warmup
     want = set(args.only) if args.only else None
 

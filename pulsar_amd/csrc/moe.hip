@@ -8,8 +8,9 @@
 //          token's slots, each slot's row dot lands in LDS and the slots
 //          are summed in slot order.
 // Grouped path (CSR by expert, pulsar_kernels.cu:2689-2789): one block per
-// (row group, expert group); the rows' weight units are loaded once into
-// registers and every (token, slot) pair of the group is dotted against them.
+// (row block, expert group); the group's pair activations are staged in LDS
+// once, and each wave streams row passes of the expert (the next pass's
+// weights in flight while the current one is dotted with every pair).
 #include "pk_rowdot.h"
 
 namespace pk {
@@ -48,8 +49,8 @@ __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
     Act a[UPLMAX];
     load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
     typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
+    load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
+    load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
     float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
     float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
     if (row_ok && rg.holds_row()) {
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                 Act a[UPLMAX];
                 load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
                 typename Fmt<Q>::W w[UPLMAX];
-                load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
+                load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
                 v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
             }
             if (rg.holds_row()) part[s - base][rg.rip] = v;
@@ -103,39 +104,108 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
     if (wave == 0 && rg.holds_row() && row_ok) out[(uint64_t)token * out_dim + row] = total;
 }
 
+#ifndef PK_GRP_PPW
+#define PK_GRP_PPW 8u  // row passes per wave in the grouped kernels
+#endif
+constexpr uint32_t kGrpActLds = 32768u;  // LDS bytes for a group's staged activations
+constexpr uint32_t kGrpMaxPairs = 16u;   // pairs staged per round
+
+// Copies the q8_K rows of pairs [c0, c0 + np) into LDS (load_act_lds
+// layout, `blocks` super-blocks per row) and their pair ids into pr_l.
+// DOWN: the row is the (token, slot)'s mid row, else the token's row.
+template <bool DOWN>
+PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const uint32_t *pairs, uint32_t c0, uint32_t np,
+                            const pulsar_block_q8_K *src, uint32_t blocks, uint32_t n_used) {
+    const uint32_t per_row = blocks * 73u;  // dwords per q8_K row
+    for (uint32_t k = threadIdx.x; k < np * per_row; k += blockDim.x) {
+        const uint32_t j = k / per_row, r = k - j * per_row;
+        const uint32_t sb = r / 73u, d = r - sb * 73u;
+        const uint32_t pr = pairs[c0 + j];
+        const uint64_t row = DOWN ? (uint64_t)(pr >> 4) * n_used + (pr & 15u) : (uint64_t)(pr >> 4);
+        const uint32_t v = ld32((const uint8_t *)(src + row * blocks) + 4u * r);
+        *(uint32_t *)(acts + j * blocks * kActLdsPitch + sb * kActLdsPitch + act_lds_offset(d)) = v;
+    }
+    for (uint32_t j = threadIdx.x; j < np; j += blockDim.x) pr_l[j] = pairs[c0 + j];
+}
+
+// Grouped kernels: one block per (row block, expert group). The group's
+// pair activations are staged in LDS once (in rounds of `pmax` pairs);
+// every wave streams PK_GRP_PPW row passes of the expert, the next pass's
+// weight loads issued before the current pass is dotted with each pair.
 template <uint32_t Q, uint32_t UPLMAX>
 __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
         float *__restrict__ mid, const pulsar_expert_ptrs *__restrict__ gptrs,
         const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
         const float *__restrict__ weights, const pulsar_block_q8_K *__restrict__ xq,
         uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t mid_dim,
-        uint32_t n_used, uint64_t row_bytes, uint32_t act_op) {
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
     PK_IQ2_LUT(Q)
+    extern __shared__ __align__(16) uint8_t acts_lds[];
+    __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
     const pulsar_expert_ptrs p = gptrs[group];
     if (!p.gate || !p.up) return;
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    if (s0 >= s1) return;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
-    const bool row_ok = row < mid_dim;
+    const uint32_t n_pass = (mid_dim + rpp - 1u) / rpp;
+    const uint32_t pass0 = (blockIdx.x * kWaves + threadIdx.x / 64u) * PK_GRP_PPW;
+    const uint32_t act_bytes = in_blocks * kActLdsPitch;
+    auto row_of = [&](uint32_t pass) {
+        const uint32_t row = pass * rpp + rg.rip;
+        return row < mid_dim ? row : 0u;
+    };
     typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.gate + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.up + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
-    const float gb = row_ok && p.gate_b ? p.gate_b[row] : 0.0f;
-    const float ub = row_ok && p.up_b ? p.up_b[row] : 0.0f;
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
-    for (uint32_t i = s0; i < s1; i++) {
-        const uint32_t pr = pairs[i];
-        const uint32_t token = pr >> 4, slot = pr & 15u;
-        const uint64_t so = (uint64_t)token * n_used + slot;
-        Act a[UPLMAX];
-        load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
-        float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
-        float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
-        if (row_ok && rg.holds_row()) {
-            if (p.gate_b) g += gb;
-            if (p.up_b) u += ub;
-            mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
+    load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)row_of(pass0) * row_bytes, rg, wg);
+    load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)row_of(pass0) * row_bytes, rg, wu);
+    for (uint32_t c0 = s0; c0 < s1; c0 += pmax) {
+        const uint32_t np = s1 - c0 < pmax ? s1 - c0 : pmax;
+        if (c0 != s0) {
+            __syncthreads();  // the previous round's activations are consumed
+            load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)row_of(pass0) * row_bytes, rg, wg);
+            load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)row_of(pass0) * row_bytes, rg, wu);
+        }
+        stage_pair_acts<false>(acts_lds, pr_l, pairs, c0, np, xq, in_blocks, n_used);
+        __syncthreads();
+        for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
+            const uint32_t pass = pass0 + k;
+            if (pass >= n_pass) break;  // wave-uniform
+            const bool more = k + 1u < PK_GRP_PPW && pass + 1u < n_pass;
+            typename Fmt<Q>::W ng[UPLMAX], nu[UPLMAX];
+            if (more) {
+                load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)row_of(pass + 1u) * row_bytes, rg, ng);
+                load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)row_of(pass + 1u) * row_bytes, rg, nu);
+            }
+            const uint32_t row = pass * rpp + rg.rip;
+            const bool row_ok = row < mid_dim;
+            const float gb = row_ok && p.gate_b ? p.gate_b[row] : 0.0f;
+            const float ub = row_ok && p.up_b ? p.up_b[row] : 0.0f;
+            for (uint32_t j = 0; j < np; j++) {
+                const uint32_t pr = pr_l[j];
+                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+#pragma unroll
+                for (uint32_t i = 0; i < UPLMAX; i++) {
+                    opaque(wg[i]);
+                    opaque(wu[i]);
+                }
+                Act a[UPLMAX];
+                load_row_acts_lds<Q, UPLMAX>(acts_lds + j * act_bytes, rg, a);
+                float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
+                float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
+                if (row_ok && rg.holds_row()) {
+                    if (p.gate_b) g += gb;
+                    if (p.up_b) u += ub;
+                    mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
+                }
+            }
+            if (more) {
+#pragma unroll
+                for (uint32_t i = 0; i < UPLMAX; i++) {
+                    wg[i] = ng[i];
+                    wu[i] = nu[i];
+                }
+            }
         }
     }
 }
@@ -146,26 +216,66 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
         const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
         const pulsar_block_q8_K *__restrict__ midq, uint32_t n_units, uint32_t nblk32,
         uint32_t lpr_log2, uint32_t mid_blocks, uint32_t out_dim, uint32_t n_used,
-        uint64_t row_bytes) {
+        uint64_t row_bytes, uint32_t pmax) {
     PK_IQ2_LUT(Q)
+    extern __shared__ __align__(16) uint8_t acts_lds[];
+    __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
     const pulsar_expert_ptrs p = gptrs[group];
     if (!p.down) return;
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    if (s0 >= s1) return;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
-    const bool row_ok = row < out_dim;
+    const uint32_t n_pass = (out_dim + rpp - 1u) / rpp;
+    const uint32_t pass0 = (blockIdx.x * kWaves + threadIdx.x / 64u) * PK_GRP_PPW;
+    const uint32_t act_bytes = mid_blocks * kActLdsPitch;
+    auto row_of = [&](uint32_t pass) {
+        const uint32_t row = pass * rpp + rg.rip;
+        return row < out_dim ? row : 0u;
+    };
     typename Fmt<Q>::W w[UPLMAX];
-    load_row_w<Q, UPLMAX>((const uint8_t *)p.down + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
-    for (uint32_t i = s0; i < s1; i++) {
-        const uint32_t pr = pairs[i];
-        const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-        Act a[UPLMAX];
-        load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
-        const float v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
-        if (row_ok && rg.holds_row()) partial[so * out_dim + row] = v;
+    load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)row_of(pass0) * row_bytes, rg, w);
+    for (uint32_t c0 = s0; c0 < s1; c0 += pmax) {
+        const uint32_t np = s1 - c0 < pmax ? s1 - c0 : pmax;
+        if (c0 != s0) {
+            __syncthreads();
+            load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)row_of(pass0) * row_bytes, rg, w);
+        }
+        stage_pair_acts<true>(acts_lds, pr_l, pairs, c0, np, midq, mid_blocks, n_used);
+        __syncthreads();
+        for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
+            const uint32_t pass = pass0 + k;
+            if (pass >= n_pass) break;  // wave-uniform
+            const bool more = k + 1u < PK_GRP_PPW && pass + 1u < n_pass;
+            typename Fmt<Q>::W nw[UPLMAX];
+            if (more) load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)row_of(pass + 1u) * row_bytes, rg, nw);
+            const uint32_t row = pass * rpp + rg.rip;
+            const bool row_ok = row < out_dim;
+            for (uint32_t j = 0; j < np; j++) {
+                const uint32_t pr = pr_l[j];
+                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+#pragma unroll
+                for (uint32_t i = 0; i < UPLMAX; i++) opaque(w[i]);
+                Act a[UPLMAX];
+                load_row_acts_lds<Q, UPLMAX>(acts_lds + j * act_bytes, rg, a);
+                const float v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
+                if (row_ok && rg.holds_row()) partial[so * out_dim + row] = v;
+            }
+            if (more) {
+#pragma unroll
+                for (uint32_t i = 0; i < UPLMAX; i++) w[i] = nw[i];
+            }
+        }
     }
+}
+
+// Pairs staged per round for rows of `blocks` super-blocks.
+static uint32_t grouped_pmax(uint32_t blocks) {
+    const uint32_t per = blocks * kActLdsPitch;
+    uint32_t pm = kGrpActLds / per;
+    if (pm < 1u) pm = 1u;
+    return pm < kGrpMaxPairs ? pm : kGrpMaxPairs;
 }
 
 // Deterministic slot reduce (pulsar_kernels.cu:2791-2806).
@@ -287,13 +397,14 @@ struct PairGroupedLaunch {
     Geo g;
     template <uint32_t Q, uint32_t U>
     int run() {
-        const uint32_t rpb = kWaves * (64u >> g.l2);
+        const uint32_t rpb = kWaves * PK_GRP_PPW * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_group);
-        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)mid,
-                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts,
+        const uint32_t pmax = grouped_pmax(g.blocks);
+        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), pmax * g.blocks * kActLdsPitch,
+                           pk::stream(), (float *)mid, (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts,
                            (const uint32_t *)pairs, (const float *)weights,
                            (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
-                           mid_dim, n_used, row_bytes, act_op);
+                           mid_dim, n_used, row_bytes, act_op, pmax);
         return launch_ok("moe pair swiglu grouped launch");
     }
 };
@@ -306,13 +417,14 @@ struct DownGroupedLaunch {
     Geo g;
     template <uint32_t Q, uint32_t U>
     int run() {
-        const uint32_t rpb = kWaves * (64u >> g.l2);
+        const uint32_t rpb = kWaves * PK_GRP_PPW * (64u >> g.l2);
         const dim3 grid((out_dim + rpb - 1u) / rpb, n_group);
-        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), 0, pk::stream(),
-                           (float *)partial, (const pulsar_expert_ptrs *)gptrs,
+        const uint32_t pmax = grouped_pmax(g.blocks);
+        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), pmax * g.blocks * kActLdsPitch,
+                           pk::stream(), (float *)partial, (const pulsar_expert_ptrs *)gptrs,
                            (const uint32_t *)starts, (const uint32_t *)pairs,
                            (const pulsar_block_q8_K *)midq, g.n_units, g.nblk32, g.l2, g.blocks,
-                           out_dim, n_used, row_bytes);
+                           out_dim, n_used, row_bytes, pmax);
         return launch_ok("moe down grouped launch");
     }
 };

@@ -34,6 +34,28 @@ static inline int reject(const char *what) {
     return 0;
 }
 
+// A pointer read from memory (expert tables) is generic to the compiler;
+// this marks it as global memory so loads through it are global loads.
+PK_DEV const uint8_t *as_global(const void *p) {
+    return (const uint8_t *)(const __attribute__((address_space(1))) uint8_t *)p;
+}
+PK_DEV const float *as_global_f(const float *p) {
+    return (const float *)(const __attribute__((address_space(1))) float *)p;
+}
+
+// Makes a register-resident value opaque to the optimiser at this point,
+// so work derived from it is not hoisted out of the enclosing loop (keeps
+// the register count of pair loops at one decode's worth).
+template <typename T>
+PK_DEV void opaque(T &v) {
+    static_assert(sizeof(T) % 4 == 0, "word-sized members");
+    uint32_t w[sizeof(T) / 4];
+    __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+    for (uint32_t i = 0; i < sizeof(T) / 4; i++) asm volatile("" : "+v"(w[i]));
+    __builtin_memcpy(&v, w, sizeof(T));
+}
+
 // ---------------------------------------------------------------- loads --
 // Weight blocks sit at 1/2/4-byte alignment inside rows (MXFP4 17 B,
 // Q6_K 210 B, IQ2_XXS 66 B, Q2_K 84 B); gfx950 global loads accept any

@@ -58,30 +58,44 @@ PK_DEV int32_t dot16(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint4 a
 }
 
 // Loads the activation slice of unit g (super-block g>>2, unit g&3) of a
-// q8_K row. ACT_STRIDE32 selects the 4 x 16 runs 32 apart (Q6_K, Q2_K).
-template <bool ACT_STRIDE32, int BS_MODE>
-PK_DEV void load_act(const pulsar_block_q8_K *xq_row, uint32_t g, Act &a) {
-    const uint8_t *blk = (const uint8_t *)(xq_row + (g >> 2));
+// q8_K row laid out with PITCH bytes per super-block, d at 0, qs at QOFF
+// and bsums at BOFF. ACT_STRIDE32 selects the 4 x 16 runs 32 apart (Q6_K,
+// Q2_K).
+// ALIGNED: the fields sit at their natural alignment (LDS copies).
+template <bool ALIGNED>
+PK_DEV uint4 ldf128(const uint8_t *p) {
+    if (ALIGNED) return *(const uint4 *)p;
+    return ld128(p);
+}
+template <bool ALIGNED>
+PK_DEV uint2 ldf64(const uint8_t *p) {
+    if (ALIGNED) return *(const uint2 *)p;
+    return ld64(p);
+}
+
+template <bool ACT_STRIDE32, int BS_MODE, uint32_t PITCH, uint32_t QOFF, uint32_t BOFF, bool ALIGNED = false>
+PK_DEV void load_act_at(const uint8_t *row, uint32_t g, Act &a) {
+    const uint8_t *blk = row + (uint64_t)(g >> 2) * PITCH;
     const uint32_t u = g & 3u;
-    a.yd = __builtin_bit_cast(float, ld32(blk));
-    const uint8_t *qs = blk + 4;
+    a.yd = ALIGNED ? *(const float *)blk : __builtin_bit_cast(float, ld32(blk));
+    const uint8_t *qs = blk + QOFF;
     if (ACT_STRIDE32) {
         const uint32_t base = 128u * (u >> 1) + 16u * (u & 1u);
 #pragma unroll
-        for (int s = 0; s < 4; s++) a.q[s] = ld128(qs + base + 32u * s);
+        for (int s = 0; s < 4; s++) a.q[s] = ldf128<ALIGNED>(qs + base + 32u * s);
     } else {
 #pragma unroll
-        for (int s = 0; s < 4; s++) a.q[s] = ld128(qs + 64u * u + 16u * s);
+        for (int s = 0; s < 4; s++) a.q[s] = ldf128<ALIGNED>(qs + 64u * u + 16u * s);
     }
-    const uint8_t *bs = blk + 260;
+    const uint8_t *bs = blk + BOFF;
     if (BS_MODE == 1) {  // Q4_K: bsums[4u .. 4u+3]
-        const uint2 v = ld64(bs + 8u * u);
+        const uint2 v = ldf64<ALIGNED>(bs + 8u * u);
         a.bs[0] = sext16(v.x);
         a.bs[1] = sext16(v.x >> 16);
         a.bs[2] = sext16(v.y);
         a.bs[3] = sext16(v.y >> 16);
     } else if (BS_MODE == 2) {  // Q2_K / Q6_K: bsums[8(u>>1) + (u&1) + 2s]
-        const uint4 v = ld128(bs + 16u * (u >> 1));
+        const uint4 v = ldf128<ALIGNED>(bs + 16u * (u >> 1));
         const uint32_t o = u & 1u;
         a.bs[0] = sext16(word_of(v, 0) >> (16u * o));
         a.bs[1] = sext16(word_of(v, 1) >> (16u * o));
@@ -90,6 +104,23 @@ PK_DEV void load_act(const pulsar_block_q8_K *xq_row, uint32_t g, Act &a) {
     } else {
         a.bs[0] = a.bs[1] = a.bs[2] = a.bs[3] = 0;
     }
+}
+
+// From a q8_K row in global memory (292-byte blocks).
+template <bool ACT_STRIDE32, int BS_MODE>
+PK_DEV void load_act(const pulsar_block_q8_K *xq_row, uint32_t g, Act &a) {
+    load_act_at<ACT_STRIDE32, BS_MODE, 292u, 4u, 260u>((const uint8_t *)xq_row, g, a);
+}
+
+// LDS copy of a q8_K row: 304-byte blocks, d at 0, qs at 16 (16-byte
+// aligned), bsums at 272. Source dword k of a block lands at byte
+// (k == 0 ? 0 : 4k + 12).
+constexpr uint32_t kActLdsPitch = 304u;
+PK_DEV uint32_t act_lds_offset(uint32_t k) { return k == 0 ? 0u : 4u * k + 12u; }
+
+template <bool ACT_STRIDE32, int BS_MODE>
+PK_DEV void load_act_lds(const uint8_t *row, uint32_t g, Act &a) {
+    load_act_at<ACT_STRIDE32, BS_MODE, kActLdsPitch, 16u, 272u, true>(row, g, a);
 }
 
 template <uint32_t Q>

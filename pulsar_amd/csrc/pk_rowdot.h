@@ -69,6 +69,16 @@ PK_DEV void load_row_acts(const pulsar_block_q8_K *xq_row, const RowGeom &rg, Ac
     }
 }
 
+// The same from an LDS copy of the row (load_act_lds layout).
+template <uint32_t Q, uint32_t UPLMAX>
+PK_DEV void load_row_acts_lds(const uint8_t *row, const RowGeom &rg, Act (&a)[UPLMAX]) {
+#pragma unroll
+    for (uint32_t i = 0; i < UPLMAX; i++) {
+        const uint32_t g = rg.lir + (i << rg.lpr_log2);
+        if ((g & ~3u) < rg.n_units) load_act_lds<Fmt<Q>::kStride32, Fmt<Q>::kBsMode>(row, g, a[i]);
+    }
+}
+
 // Loads this lane's weight units of one row. Loads are unconditional: a
 // lane whose unit does not exist reads the row's last unit instead (in
 // bounds) and row_partial masks its contribution; callers likewise pass a

@@ -45,72 +45,133 @@ __global__ __launch_bounds__(256) void route_ptrs_kernel(pulsar_expert_ptrs *__r
     slot_w[i] = w;
 }
 
-// One block; every pair's group rank and destination are counted directly
-// (n <= 2048 pairs, so the quadratic counts stay in the microseconds).
-__global__ __launch_bounds__(1024) void group_csr_kernel(pulsar_expert_ptrs *__restrict__ gptrs,
-                                                         uint32_t *__restrict__ starts,
-                                                         uint32_t *__restrict__ pairs,
-                                                         const pulsar_expert_ptrs *__restrict__ ptrs,
-                                                         uint32_t n, uint32_t n_used,
-                                                         uint32_t max_groups) {
-    __shared__ uint64_t key[kMaxCsrPairs];
-    __shared__ uint16_t first[kMaxCsrPairs];  // index of the first pair with the same gate
-    __shared__ uint16_t grp[kMaxCsrPairs];    // group id (0xffff: NULL gate)
-    __shared__ uint32_t n_groups, n_pairs;
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    for (uint32_t i = tid; i < n; i += nt) key[i] = (uint64_t)(uintptr_t)ptrs[i].gate;
-    if (tid == 0) {
-        n_groups = 0;
-        n_pairs = 0;
+constexpr uint32_t kCsrThreads = 1024;  // two pairs per thread
+constexpr uint32_t kHashSlots = 4096;    // open-addressing table, >= 2 x kMaxCsrPairs
+
+// Exclusive block-wide scan of two consecutive elements per thread (2 tid,
+// 2 tid + 1); returns the total. Contains two block barriers.
+PK_DEV uint32_t block_scan2(uint32_t v0, uint32_t v1, uint32_t &e0, uint32_t &e1, uint32_t *wsum) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t own = v0 + v1;
+    uint32_t s = own;
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const uint32_t o = __shfl_up(s, d, 64);
+        if (lane >= d) s += o;
+    }
+    if (lane == 63u) wsum[wave] = s;
+    __syncthreads();
+    uint32_t base = 0, total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kCsrThreads / 64u; w++) {
+        const uint32_t x = wsum[w];
+        base += w < wave ? x : 0u;
+        total += x;
+    }
+    e0 = base + s - own;
+    e1 = e0 + v0;
+    __syncthreads();
+    return total;
+}
+
+PK_DEV uint32_t ptr_hash(uint64_t k) { return (uint32_t)(((k >> 4) * 0x9E3779B97F4A7C15ull) >> 52); }
+
+// Groups the (token, slot) pairs by expert (gate pointer) in order of first
+// appearance, pairs of a group in pair order, like the reference's host
+// grouping (crates/engine/src/lib.rs:8357-8392). One block; every step has
+// constant depth: first occurrences through an LDS hash table (atomic CAS
+// insert, atomic min of the pair index), group ids and group starts by
+// block scans, members scattered to their group's segment and put in pair
+// order by counting the smaller pair indices in the segment.
+__global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_ptrs *__restrict__ gptrs,
+                                                               uint32_t *__restrict__ starts,
+                                                               uint32_t *__restrict__ pairs,
+                                                               const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                               uint32_t n, uint32_t n_used, uint32_t max_groups) {
+    __shared__ unsigned long long tkey[kHashSlots];
+    __shared__ uint32_t tfirst[kHashSlots];
+    __shared__ uint32_t gid_of[kMaxCsrPairs];  // group id, at the index of the group's first pair
+    __shared__ uint32_t gstart[kMaxCsrPairs + 1];
+    __shared__ uint32_t fill[kMaxCsrPairs];
+    __shared__ uint32_t seg[kMaxCsrPairs];  // pair indices by group, unordered within a group
+    __shared__ uint32_t wsum[kCsrThreads / 64u];
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t h = tid; h < kHashSlots; h += kCsrThreads) {
+        tkey[h] = 0ull;
+        tfirst[h] = UINT32_MAX;
+    }
+    for (uint32_t g = tid; g < kMaxCsrPairs; g += kCsrThreads) {
+        gstart[g] = 0u;
+        fill[g] = 0u;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += nt) {
-        uint32_t f = i;
-        if (key[i] != 0)
-            for (uint32_t j = 0; j < i; j++)
-                if (key[j] == key[i]) {
-                    f = j;
-                    break;
-                }
-        first[i] = (uint16_t)f;
-    }
-    __syncthreads();
-    // group id = number of distinct gates first seen before this group's first pair
-    for (uint32_t i = tid; i < n; i += nt) {
-        uint16_t g = 0xffffu;
-        if (key[i] != 0) {
-            const uint32_t f = first[i];
-            uint32_t r = 0;
-            for (uint32_t j = 0; j < f; j++) r += (key[j] != 0 && first[j] == j) ? 1u : 0u;
-            g = (uint16_t)r;
-        }
-        grp[i] = g;
-        if (key[i] != 0) {
-            atomicAdd(&n_pairs, 1u);
-            if (first[i] == i) atomicAdd(&n_groups, 1u);
+
+    uint64_t key[2];
+    uint32_t slot[2] = {0u, 0u};
+#pragma unroll
+    for (uint32_t e = 0; e < 2; e++) {
+        const uint32_t i = 2u * tid + e;
+        key[e] = i < n ? (uint64_t)(uintptr_t)ptrs[i].gate : 0ull;
+        if (key[e] != 0ull) {
+            uint32_t h = ptr_hash(key[e]);
+            for (;;) {  // the table has more free slots than pairs: ends
+                const unsigned long long prev = atomicCAS(&tkey[h], 0ull, (unsigned long long)key[e]);
+                if (prev == 0ull || prev == key[e]) break;
+                h = (h + 1u) & (kHashSlots - 1u);
+            }
+            atomicMin(&tfirst[h], i);
+            slot[e] = h;
         }
     }
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += nt) {
-        const uint32_t g = grp[i];
-        if (g == 0xffffu) continue;
-        // destination = pairs ordered by (group, pair index)
-        uint32_t dst = 0;
-        for (uint32_t j = 0; j < n; j++) {
-            const uint32_t gj = grp[j];
-            dst += (gj != 0xffffu && (gj < g || (gj == g && j < i))) ? 1u : 0u;
-        }
-        pairs[dst] = ((i / n_used) << 4) | (i % n_used);
-        if (first[i] == i && g < max_groups) {
-            starts[g] = dst;
+    uint32_t first[2], isf[2];
+#pragma unroll
+    for (uint32_t e = 0; e < 2; e++) {
+        first[e] = key[e] != 0ull ? tfirst[slot[e]] : UINT32_MAX;
+        isf[e] = first[e] == 2u * tid + e ? 1u : 0u;
+    }
+    uint32_t g0, g1;
+    const uint32_t n_groups = block_scan2(isf[0], isf[1], g0, g1, wsum);
+    if (isf[0]) gid_of[2u * tid] = g0;
+    if (isf[1]) gid_of[2u * tid + 1u] = g1;
+    __syncthreads();
+    uint32_t grp[2];
+#pragma unroll
+    for (uint32_t e = 0; e < 2; e++) {
+        grp[e] = key[e] != 0ull ? gid_of[first[e]] : UINT32_MAX;
+        if (key[e] != 0ull) atomicAdd(&gstart[grp[e]], 1u);  // member count for now
+    }
+    __syncthreads();
+    uint32_t c0 = gstart[2u * tid], c1 = gstart[2u * tid + 1u], s0, s1;
+    const uint32_t n_pairs = block_scan2(c0, c1, s0, s1, wsum);
+    gstart[2u * tid] = s0;
+    gstart[2u * tid + 1u] = s1;
+    if (tid == 0) gstart[kMaxCsrPairs] = n_pairs;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t e = 0; e < 2; e++)
+        if (key[e] != 0ull) seg[gstart[grp[e]] + atomicAdd(&fill[grp[e]], 1u)] = 2u * tid + e;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t e = 0; e < 2; e++) {
+        if (key[e] == 0ull) continue;
+        const uint32_t i = 2u * tid + e, g = grp[e], st = gstart[g], len = fill[g];
+        uint32_t r = 0;
+        for (uint32_t q = 0; q < len; q++) r += seg[st + q] < i ? 1u : 0u;
+        pairs[st + r] = ((i / n_used) << 4) | (i % n_used);
+        if (isf[e] && g < max_groups) {
+            starts[g] = st;
             gptrs[g] = ptrs[i];
         }
     }
-    for (uint32_t g = n_groups + tid; g < max_groups; g += nt) {
+    // group slots past the last group: NULL with empty ranges. Groups past
+    // max_groups (a too-small bound from the caller) are not reachable.
+    const uint32_t end = n_groups > max_groups ? gstart[max_groups] : n_pairs;
+    for (uint32_t g = n_groups + tid; g < max_groups; g += kCsrThreads) {
         gptrs[g] = pulsar_expert_ptrs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-        starts[g] = n_pairs;
+        starts[g] = end;
     }
-    if (tid == 0) starts[max_groups] = n_pairs;
+    if (tid == 0) starts[max_groups] = end;
 }
 
 }  // namespace pk
@@ -136,7 +197,7 @@ extern "C" int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, cons
     if (!gptrs || !starts || !pairs || !ptrs || n_tok == 0 || n_used == 0 || n_used > 16u ||
         max_groups == 0 || (uint64_t)n_tok * n_used > pk::kMaxCsrPairs)
         return pk::reject("moe group csr");
-    hipLaunchKernelGGL(pk::group_csr_kernel, dim3(1), dim3(1024), 0, pk::stream(), (pulsar_expert_ptrs *)gptrs,
+    hipLaunchKernelGGL(pk::group_csr_kernel, dim3(1), dim3(pk::kCsrThreads), 0, pk::stream(), (pulsar_expert_ptrs *)gptrs,
                        (uint32_t *)starts, (uint32_t *)pairs, (const pulsar_expert_ptrs *)ptrs,
                        n_tok * n_used, n_used, max_groups);
     return pk::launch_ok("moe group csr launch");

@@ -253,12 +253,13 @@ def test_matmul_f32_and_bias(dev):
 
 # ------------------------------------------------- device routing, graphs --
 
-def test_route_ptrs_and_group_csr(dev):
-    E, k, n_tok, hidden, ffn = 12, 6, 20, 256, 256
+@pytest.mark.parametrize("E,k,n_tok", [(12, 6, 20), (300, 15, 128), (4, 1, 2)])
+def test_route_ptrs_and_group_csr(dev, E, k, n_tok):
+    hidden, ffn = 256, 256
     L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=hidden, ffn=ffn, E=E, n_used=k, n_tok=n_tok, biases=True)
     sel = rng.integers(0, E, (n_tok, k)).astype(np.int32)
-    sel[3, 2] = -1  # unrouted
-    sel[7, 0] = E + 5  # out of range -> NULL
+    sel[n_tok // 2, k // 2] = -1  # unrouted
+    sel[n_tok - 1, 0] = E + 5  # out of range -> NULL
     rw = rng.uniform(0.1, 1, (n_tok, k)).astype(np.float32)
     gsz, dsz = ffn * L.grb, hidden * L.drb
     bank = K.ExpertBank(L.dg.data_ptr(), L.du.data_ptr(), L.dd.data_ptr(), L.dbias[0].data_ptr(),
