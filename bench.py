@@ -185,7 +185,10 @@ class DevLayer:
         )
 
 
-def bench_moe(ctx, spec, steps, warmup, grouped: bool):
+def bench_moe(ctx, spec, steps, warmup, path: str):
+    """One whole layer per step. path: "plain" (reference entry points with
+    device routing), "grouped" (CSR by expert, grouped kernels) or "fused"
+    (router_logits_q8 + moe_pair_routed + moe_down_f32: three launches)."""
     torch, K, fm = ctx["torch"], ctx["K"], ctx["fm"]
     s = spec
     bank_bytes = s.n_expert * s.expert_bytes
@@ -219,6 +222,14 @@ def bench_moe(ctx, spec, steps, warmup, grouped: bool):
         b = L.banks[i % n_banks]
         x = xs[i % n_x]
         sel = sel_all[i]
+        if path == "fused":
+            K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+            K.moe_pair_routed(mid, ptrs, slot_w, sel, rw, logits, None, s.n_expert, s.k_used, 1.0, 1,
+                              descs[i % n_banks], shared[i % n_banks] if shared else None, xq, s.hidden, s.ffn,
+                              s.n_tok, s.gate_row_bytes, s.gate_quant, s.act_op)
+            K.moe_down_f32(out, ptrs, slot_w, mid, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
+                           s.down_quant, s.biases)
+            return
         K.matmul_f32(logits, b["router_w"], x, s.hidden, s.n_expert, s.n_tok)
         if b["router_b"] is not None:
             K.add_bias_rows(logits, b["router_b"], s.n_expert, s.n_tok)
@@ -226,7 +237,7 @@ def bench_moe(ctx, spec, steps, warmup, grouped: bool):
         K.moe_route_ptrs(ptrs, slot_w, sel, rw, descs[i % n_banks], s.n_expert,
                          shared[i % n_banks] if shared else None, s.n_tok, s.k_used)
         K.quantize_q8_k(xq, x, s.hidden, s.n_tok)
-        if grouped:
+        if path == "grouped":
             K.moe_group_csr(gptrs, starts, pairs, ptrs, s.n_tok, n_slots, max_groups)
             K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq, s.hidden, s.ffn, n_slots,
                                       max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
@@ -251,7 +262,7 @@ def bench_moe(ctx, spec, steps, warmup, grouped: bool):
     router_bytes = s.n_expert * s.hidden * 4 + (s.n_expert * 4 if s.biases else 0)
     alg = float(np.mean(distinct)) * (s.expert_bytes + bias_bytes) + router_bytes + act_bytes
     res = {
-        "path": "grouped" if grouped else "plain",
+        "path": path,
         "n_tok": s.n_tok,
         "us_per_layer": ms * 1e3,
         "us_per_token": ms * 1e3 / s.n_tok,
@@ -407,10 +418,13 @@ def main():
         results["c2_q6k_8192x4096_chunk16"] = bench_matvec(ctx, "c2c", fm.QUANT_Q6_K, 8192, 4096, 16, steps,
                                                            warmup)
     layer_steps = max(20, steps // 2)
-    for spec, grouped in ((synth.C3, False), (synth.C4_Q2K, True), (synth.C4_IQ2, True),
-                          (synth.C5_B1, False), (synth.C5_B64, False)):
+    for spec, path in ((synth.C3, "fused"), (synth.C4_Q2K, "grouped"), (synth.C4_IQ2, "grouped"),
+                       (synth.C5_B1, "fused"), (synth.C5_B64, "plain")):
         if on(spec.name):
-            results[spec.name] = bench_moe(ctx, spec, layer_steps, warmup, grouped)
+            results[spec.name] = bench_moe(ctx, spec, layer_steps, warmup, path)
+        # the same layer through the reference's own (unfused) entry points
+        if path == "fused" and on(spec.name + "_unfused"):
+            results[spec.name + "_unfused"] = bench_moe(ctx, spec, layer_steps, warmup, "plain")
     peak = stream_peak(ctx) if want is None else None
 
     head = results.get(HEADLINE) or next(iter(results.values()))

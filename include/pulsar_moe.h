@@ -202,6 +202,41 @@ int pulsar_moe_route_ptrs(void *ptrs, void *slot_weights, const void *selected,
 int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, const void *ptrs,
                          uint32_t n_tok, uint32_t n_used, uint32_t max_groups);
 
+/* ---- fused decode layer (no reference counterpart: the reference runs
+ * these steps as separate launches with a host round trip in between,
+ * crates/engine/src/lib.rs:7663-7670, 8416-8510). Each call produces
+ * exactly the bytes of the separate calls it replaces. */
+
+/* pulsar_matmul_f32(logits, w_r, x) [+ pulsar_add_bias_rows(logits, bias)
+ * when bias != NULL] + pulsar_quantize_q8_K(xq, x, in_dim, n_tok), one
+ * launch. */
+int pulsar_router_logits_q8(void *logits, void *xq, const void *x, const void *w_r,
+                            const void *bias, uint32_t in_dim, uint32_t n_expert,
+                            uint32_t n_tok);
+
+/* pulsar_router_select (softmax_mode 0 or 1, no sink slots) +
+ * pulsar_moe_route_ptrs + pulsar_moe_pair_swiglu, one launch: every block
+ * routes its token itself. Writes selected / weights [n_tok][k_used],
+ * ptrs / slot_weights [n_tok][k_used + n_shared] and mid
+ * [n_tok][k_used + n_shared][mid_dim]. k_used + n_shared <= 64,
+ * n_shared <= 4; bank and shared are host pointers read at launch. */
+int pulsar_moe_pair_routed(void *mid, void *ptrs, void *slot_weights, void *selected,
+                           void *weights, const void *logits, const void *router_bias,
+                           uint32_t n_expert, uint32_t k_used, float weight_scale,
+                           uint32_t softmax_mode, const pulsar_expert_bank *bank,
+                           const pulsar_expert_ptrs *shared, uint32_t n_shared,
+                           const void *xq, uint32_t in_dim, uint32_t mid_dim, uint32_t n_tok,
+                           uint64_t row_bytes, uint32_t quant, uint32_t act_op);
+
+/* pulsar_quantize_q8_K(midq, mid, mid_dim, n_tok * n_used) +
+ * pulsar_moe_down(out, ptrs, midq, ...) [+ pulsar_moe_down_bias(out, ptrs,
+ * slot_weights) when add_bias], one launch; mid is f32
+ * [n_tok][n_used][mid_dim]. The token's staged q8_K rows must fit 64 KiB
+ * (n_used * ceil(mid_dim / 256) <= 215). */
+int pulsar_moe_down_f32(void *out, const void *ptrs, const void *slot_weights, const void *mid,
+                        uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint32_t n_tok,
+                        uint64_t row_bytes, uint32_t quant, uint32_t add_bias);
+
 /* Selects the stream every later launch from the calling thread goes to
  * (NULL restores the null stream, the default). No counterpart in the
  * reference, whose launches always use the per-thread default stream

@@ -35,6 +35,10 @@ SIGNATURES = {
     "pulsar_moe_route_ptrs": [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32],
     "pulsar_moe_group_csr": [_vp, _vp, _vp, _vp, _u32, _u32, _u32],
     "pulsar_set_stream": [_vp],
+    "pulsar_router_logits_q8": [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32],
+    "pulsar_moe_pair_routed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp, _u32,
+                               _vp, _u32, _u32, _u32, _u64, _u32, _u32],
+    "pulsar_moe_down_f32": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u64, _u32, _u32],
 }
 
 _lib: ctypes.CDLL | None = None

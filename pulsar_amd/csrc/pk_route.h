@@ -1,0 +1,184 @@
+// pk_route.h - routing helpers shared by the router kernels and the fused
+// decode-layer kernels: scores, the wave-wide top-k, expert pointers.
+#pragma once
+
+#include "pk_common.h"
+
+namespace pk {
+
+// sigmoid as pulsar_kernels.cu:913-921
+PK_DEV float router_sigmoid(float x) {
+    if (x >= 0.0f) {
+        const float e = expf(-x);
+        return 1.0f / (1.0f + e);
+    }
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+constexpr uint32_t kMaxPerLane = 16;  // 64 lanes x 16 = 1024 routed logits
+
+// Order-preserving key of a routing score: larger score <=> larger key,
+// -0 and +0 equal, every non-NaN score >= 1 and NaN 0. The reference's
+// comparator (pulsar_kernels.cu:922-925) lets the higher score win, ties
+// going to the lower expert index, and never picks a NaN.
+PK_DEV uint32_t score_key(float v) {
+    if (v != v) return 0u;
+    const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);  // -0 -> +0
+    return ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) + 1u;
+}
+
+PK_DEV uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (uint32_t s = 1; s < 64u; s <<= 1) {
+        const uint32_t o = (uint32_t)partner((int32_t)v, s);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// The k rounds of the reference's top-k (pulsar_kernels.cu:938-1010) for
+// one token, by one wave. Lane l holds experts lJ .. lJ+J-1, so a lower
+// lane means a lower expert index. Each round takes the wave maximum of the
+// lanes' best keys; the lowest lane holding it owns the winner (highest
+// score, lowest index on ties), which it replaces by -inf like the
+// reference, so an expert can win again once every remaining score is
+// -inf. Winner number k lands in lane k % 64, slot k / 64 of win / wprob
+// (index, or -1 when every score is NaN; its prob, the raw logit in mode
+// 2). `sum` is the sequential sum of the winners' probs, `wmax` their max.
+template <uint32_t J>
+PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uint32_t k_used, uint32_t mode,
+                      int32_t (&win)[J], float (&wprob)[J], float &sum, float &wmax) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t kNegInf = score_key(-INFINITY);
+    uint32_t key[J];
+    float prob[J];
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane * J + j;
+        win[j] = -1;
+        wprob[j] = 0.0f;
+        if (e < n_expert) {
+            const float raw = lg[e];
+            const float p = mode == 1u ? raw : router_sigmoid(raw);
+            prob[j] = mode == 2u ? raw : p;  // mode 2 weights use the raw winner logit
+            key[j] = score_key(p + (bias ? bias[e] : 0.0f));
+        } else {
+            prob[j] = 0.0f;
+            key[j] = 0u;
+        }
+    }
+    // this lane's best: first (lowest index) maximal key
+    uint32_t bk = 0u, bj = 0u;
+    float bp = 0.0f;
+    auto lane_best = [&]() {
+        bk = 0u;
+        bj = 0u;
+        bp = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < J; j++)
+            if (key[j] > bk) {
+                bk = key[j];
+                bj = j;
+                bp = prob[j];
+            }
+    };
+    lane_best();
+    sum = 0.0f;
+    wmax = -INFINITY;
+    for (uint32_t k = 0; k < k_used; k++) {
+        const uint32_t m = wave_max_u32(bk);
+        int32_t w_e = -1;  // no candidate: every routed score is NaN
+        float w_p = 0.0f;
+        if (m != 0u) {
+            const uint64_t bal = __ballot(bk == m);
+            const int f = __builtin_ctzll(bal);
+            w_e = __builtin_amdgcn_readlane((int)(lane * J + bj), f);
+            w_p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bp), f));
+            if ((int)lane == f) {
+#pragma unroll
+                for (uint32_t j = 0; j < J; j++)
+                    if (j == bj) key[j] = kNegInf;
+                lane_best();
+            }
+        }
+        if (lane == (k & 63u)) {
+#pragma unroll
+            for (uint32_t j = 0; j < J; j++)
+                if (j == (k >> 6)) {
+                    win[j] = w_e;
+                    wprob[j] = w_p;
+                }
+        }
+        sum += w_p;
+        wmax = fmaxf(wmax, w_p);
+    }
+}
+
+// f32 GEMV for router logits: one wave per (row, group of TG tokens);
+// lanes stride over K with 16-byte loads of the row and of the TG token
+// vectors, then a wave reduction per token; bias (if any) is added to the
+// finished sum, as a separate bias pass would. Waves of a block take
+// consecutive rows of the same token group, so the token vectors are shared
+// through the cache.
+template <uint32_t TG>
+PK_DEV void gemv_wave(float *__restrict__ out, const float *__restrict__ w, const float *__restrict__ x,
+                      const float *__restrict__ bias, uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
+                      uint32_t gw, uint32_t n_work) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (gw >= n_work) return;  // wave-uniform
+    const uint32_t row = gw % out_dim, t0 = (gw / out_dim) * TG;
+    const float *wr = w + (uint64_t)row * in_dim;
+    const float *xr[TG];
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) xr[t] = x + (uint64_t)(t0 + t < n_tok ? t0 + t : n_tok - 1u) * in_dim;
+    float acc[TG];
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) acc[t] = 0.0f;
+    const uint32_t n4 = in_dim / 4u;
+    for (uint32_t i = lane; i < n4; i += 64u) {
+        const uint4 a = ld128((const uint8_t *)(wr + 4u * i));
+#pragma unroll
+        for (uint32_t t = 0; t < TG; t++) {
+            const uint4 b = ld128((const uint8_t *)(xr[t] + 4u * i));
+            acc[t] += __uint_as_float(a.x) * __uint_as_float(b.x);
+            acc[t] += __uint_as_float(a.y) * __uint_as_float(b.y);
+            acc[t] += __uint_as_float(a.z) * __uint_as_float(b.z);
+            acc[t] += __uint_as_float(a.w) * __uint_as_float(b.w);
+        }
+    }
+    for (uint32_t i = 4u * n4 + lane; i < in_dim; i += 64u) {
+#pragma unroll
+        for (uint32_t t = 0; t < TG; t++) acc[t] += wr[i] * xr[t][i];
+    }
+    const float b = bias ? bias[row] : 0.0f;
+#pragma unroll
+    for (uint32_t t = 0; t < TG; t++) {
+        float v = group_sum<64>(acc[t]);
+        if (bias) v += b;
+        if (lane == 0 && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = v;
+    }
+}
+
+constexpr uint32_t kMaxShared = 4;
+
+struct SharedSlots {
+    pulsar_expert_ptrs p[kMaxShared];
+};
+
+// Expert e's pointers in a bank (NULL record when e is out of range).
+PK_DEV pulsar_expert_ptrs bank_ptrs(const pulsar_expert_bank &bank, uint32_t n_expert, int32_t e) {
+    pulsar_expert_ptrs p = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    if (e >= 0 && (uint32_t)e < n_expert) {
+        const uint64_t ue = (uint64_t)e;
+        p.gate = (const uint8_t *)bank.gate + ue * bank.gate_stride;
+        p.up = (const uint8_t *)bank.up + ue * bank.up_stride;
+        p.down = (const uint8_t *)bank.down + ue * bank.down_stride;
+        if (bank.gate_b) p.gate_b = bank.gate_b + ue * bank.gate_b_stride;
+        if (bank.up_b) p.up_b = bank.up_b + ue * bank.up_b_stride;
+        if (bank.down_b) p.down_b = bank.down_b + ue * bank.down_b_stride;
+    }
+    return p;
+}
+
+}  // namespace pk

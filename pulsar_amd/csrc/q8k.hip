@@ -1,63 +1,21 @@
 // q8k.hip - f32 -> q8_K activation quantizer and the streaming-read probe.
-#include "pk_common.h"
+#include "pk_q8k.h"
 
 namespace pk {
 
 static thread_local hipStream_t g_stream = nullptr;
 hipStream_t stream() { return g_stream; }
 
-// One wave per 256-value block; lane l owns values 4l .. 4l+3.
-// Algorithm of the CPU lane (crates/quant/src/cpu_dot.rs:26-50):
-//   amax = max |x|; amax == 0 -> d = 0, all quants 0;
-//   d = amax / 127, inv = 127 / amax (IEEE division, correctly rounded),
-//   q = clamp(round_half_away(x * inv), -127, 127), bsums = sums of 16.
-// Values past in_dim in the tail block are 0 (pulsar_kernels.cu:1499-1501).
+// One wave per 256-value block (quantize_block_wave).
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(pulsar_block_q8_K *__restrict__ out,
                                                            const float *__restrict__ x,
                                                            uint32_t in_dim, uint32_t nb,
                                                            uint64_t n_blocks) {
     const uint64_t gblk = (uint64_t)blockIdx.x * (blockDim.x / 64u) + threadIdx.x / 64u;
     if (gblk >= n_blocks) return;  // whole wave
-    const uint32_t lane = threadIdx.x & 63u;
     const uint64_t row = gblk / nb;
     const uint32_t b = (uint32_t)(gblk - row * nb);
-    const uint32_t c0 = b * 256u + 4u * lane;
-    const float *xr = x + row * in_dim;
-    float v[4];
-    if (c0 + 4u <= in_dim) {
-        const uint4 w = ld128((const uint8_t *)(xr + c0));
-        v[0] = __uint_as_float(w.x);
-        v[1] = __uint_as_float(w.y);
-        v[2] = __uint_as_float(w.z);
-        v[3] = __uint_as_float(w.w);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = c0 + j < in_dim ? xr[c0 + j] : 0.0f;
-    }
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = wave_max(am);
-    uint8_t *ob = (uint8_t *)(out + gblk);
-    uint32_t packed = 0;
-    int32_t s4 = 0;
-    float d = 0.0f;
-    if (am != 0.0f) {
-        d = am / 127.0f;
-        const float inv = 127.0f / am;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float q = roundf(v[j] * inv);
-            // Rust's saturating `as i8` maps NaN (0 * inf when 127/amax
-            // overflows) to 0
-            q = q != q ? 0.0f : fminf(fmaxf(q, -127.0f), 127.0f);
-            const int32_t qi = (int32_t)q;
-            s4 += qi;
-            packed |= ((uint32_t)qi & 0xffu) << (8 * j);
-        }
-    }
-    *(uint32_t *)(ob + 4 + 4 * lane) = packed;
-    s4 = group_sum<4>(s4);
-    if ((lane & 3u) == 0u) *(int16_t *)(ob + 260 + 2 * (lane >> 2)) = (int16_t)s4;
-    if (lane == 0) *(float *)ob = d;
+    quantize_block_wave<4u, 260u>(x + row * in_dim, in_dim, b, (uint8_t *)(out + gblk));
 }
 
 // Streaming read through the CUs (pulsar_kernels.cu:4875-4893): every

@@ -2,16 +2,12 @@
 // from the router's ids, and the grouped-path CSR built from those pointers.
 // The reference does both on the host after a device->host copy of the ids
 // (crates/engine/src/lib.rs:7663-7670, 8255-8344, 8357-8392).
-#include "pk_common.h"
+#include "pk_route.h"
 
 namespace pk {
 
-constexpr uint32_t kMaxShared = 4;
 constexpr uint32_t kMaxCsrPairs = 2048;
 
-struct SharedSlots {
-    pulsar_expert_ptrs p[kMaxShared];
-};
 
 __global__ __launch_bounds__(256) void route_ptrs_kernel(pulsar_expert_ptrs *__restrict__ ptrs,
                                                          float *__restrict__ slot_w,
@@ -24,20 +20,11 @@ __global__ __launch_bounds__(256) void route_ptrs_kernel(pulsar_expert_ptrs *__r
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (uint64_t)n_tok * n_slots) return;
     const uint32_t t = (uint32_t)(i / n_slots), s = (uint32_t)(i % n_slots);
-    pulsar_expert_ptrs p = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    pulsar_expert_ptrs p;
     float w = 1.0f;
     if (s < k_used) {
-        const int32_t e = selected[(uint64_t)t * k_used + s];
         w = router_w[(uint64_t)t * k_used + s];
-        if (e >= 0 && (uint32_t)e < n_expert) {
-            const uint64_t ue = (uint64_t)e;
-            p.gate = (const uint8_t *)bank.gate + ue * bank.gate_stride;
-            p.up = (const uint8_t *)bank.up + ue * bank.up_stride;
-            p.down = (const uint8_t *)bank.down + ue * bank.down_stride;
-            if (bank.gate_b) p.gate_b = bank.gate_b + ue * bank.gate_b_stride;
-            if (bank.up_b) p.up_b = bank.up_b + ue * bank.up_b_stride;
-            if (bank.down_b) p.down_b = bank.down_b + ue * bank.down_b_stride;
-        }
+        p = bank_ptrs(bank, n_expert, selected[(uint64_t)t * k_used + s]);
     } else {
         p = shared.p[s - k_used];
     }

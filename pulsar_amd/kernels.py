@@ -162,6 +162,41 @@ def moe_group_csr(gptrs, starts, pairs, ptrs, n_tok: int, n_used: int, max_group
     )
 
 
+def _shared_array(shared):
+    shared = list(shared or [])
+    arr = (_Ptrs6 * max(1, len(shared)))()
+    for i, e in enumerate(shared):
+        e = tuple(e) + (0,) * (6 - len(e))
+        arr[i] = _Ptrs6(*[int(v) or None for v in e])
+    return arr, len(shared)
+
+
+# ---- fused decode layer (extensions; each equals the separate calls it replaces)
+
+def router_logits_q8(logits, xq, x, w_r, bias, in_dim: int, n_expert: int, n_tok: int) -> None:
+    """matmul_f32 [+ add_bias_rows] + quantize_q8_k(x) in one launch."""
+    _check(_lib.load().pulsar_router_logits_q8(_ptr(logits), _ptr(xq), _ptr(x), _ptr(w_r), _ptr(bias), in_dim,
+                                               n_expert, n_tok), "router_logits_q8")
+
+
+def moe_pair_routed(mid, ptrs, slot_weights, selected, weights, logits, router_bias, n_expert: int, k_used: int,
+                    weight_scale: float, softmax_mode: int, bank: ExpertBank, shared, xq, in_dim: int,
+                    mid_dim: int, n_tok: int, row_bytes: int, quant: int, act_op: int) -> None:
+    """router_select (modes 0/1) + moe_route_ptrs + moe_pair_swiglu in one launch."""
+    arr, n_shared = _shared_array(shared)
+    _check(_lib.load().pulsar_moe_pair_routed(
+        _ptr(mid), _ptr(ptrs), _ptr(slot_weights), _ptr(selected), _ptr(weights), _ptr(logits), _ptr(router_bias),
+        n_expert, k_used, weight_scale, softmax_mode, ctypes.byref(bank), ctypes.cast(arr, ctypes.c_void_p),
+        n_shared, _ptr(xq), in_dim, mid_dim, n_tok, row_bytes, quant, act_op), "moe_pair_routed")
+
+
+def moe_down_f32(out, ptrs, slot_weights, mid, mid_dim: int, out_dim: int, n_used: int, n_tok: int,
+                 row_bytes: int, quant: int, add_bias: bool) -> None:
+    """quantize_q8_k(mid) + moe_down [+ moe_down_bias] in one launch."""
+    _check(_lib.load().pulsar_moe_down_f32(_ptr(out), _ptr(ptrs), _ptr(slot_weights), _ptr(mid), mid_dim, out_dim,
+                                           n_used, n_tok, row_bytes, quant, int(bool(add_bias))), "moe_down_f32")
+
+
 def set_stream(stream) -> None:
     """Routes later launches from this thread to `stream` (a torch Stream, a
     raw hipStream_t int, or None for the null stream)."""

@@ -1,0 +1,106 @@
+"""The fused decode-layer entry points against the separate ones they
+replace: every output (logits, q8_K bytes, routing, pointers, mid, out) must
+be bit-identical, since the fused kernels run the same arithmetic in the
+same order. The separate entry points are checked against the oracle in
+test_gpu_moe.py / test_gpu_q8k_matvec.py."""
+import numpy as np
+import pytest
+import torch
+
+from pulsar_amd import kernels as K
+from pulsar_amd.formats import (ACT_SILU, ACT_SWIGLU_OAI, QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K,
+                                QUANT_Q6_K, q8k_blocks)
+from tests.gpu_util import down, up_f32, zeros_f32
+from tests.test_gpu_moe import Layer
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(77)
+
+CASES = [
+    # gq, dq, hidden, ffn, E, k, n_tok, n_shared, mode, act, biases, logit_bias, select_bias
+    (QUANT_Q4_K, QUANT_Q6_K, 512, 256, 64, 8, 1, 1, 1, ACT_SILU, False, False, False),
+    (QUANT_Q4_K, QUANT_Q6_K, 1024, 256, 256, 8, 2, 1, 1, ACT_SILU, False, False, False),
+    (QUANT_MXFP4, QUANT_MXFP4, 576, 320, 8, 4, 3, 0, 1, ACT_SWIGLU_OAI, True, True, False),
+    (QUANT_Q2_K, QUANT_IQ2_XXS, 512, 512, 40, 6, 2, 0, 0, ACT_SILU, False, False, True),
+    (QUANT_IQ2_XXS, QUANT_Q2_K, 256, 768, 300, 5, 4, 2, 1, ACT_SILU, False, True, True),
+]
+
+
+def _bank(L: Layer):
+    gsz, dsz = L.ffn * L.grb, L.hidden * L.drb
+    gb, ub, db = (0 if b is None else b.data_ptr() for b in L.dbias)
+    return K.ExpertBank(L.dg.data_ptr(), L.du.data_ptr(), L.dd.data_ptr(), gb or None, ub or None, db or None,
+                        gsz, gsz, dsz, L.ffn, L.ffn, L.hidden)
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"g{c[0]}d{c[1]}h{c[2]}f{c[3]}E{c[4]}k{c[5]}t{c[6]}m{c[8]}")
+def test_fused_layer_matches_separate_calls(dev, case):
+    gq, dq, hidden, ffn, E, k, n_tok, n_sh, mode, act, biases, logit_bias, select_bias = case
+    L = Layer(gq, dq, hidden=hidden, ffn=ffn, E=E + n_sh, n_used=k, n_tok=n_tok, biases=biases)
+    # routed experts 0..E-1; shared experts are the last n_sh of the bank
+    shared = [L.dev_entries(E + i) for i in range(n_sh)]
+    bank = _bank(L)
+    n_slots = k + n_sh
+    f32 = dict(dtype=torch.float32, device=dev)
+    x = torch.from_numpy(rng.standard_normal((n_tok, hidden)).astype(np.float32)).to(dev)
+    if n_tok > 1:
+        x[-1] = float("nan") if mode == 1 else x[-1]  # an all-NaN token routes nowhere
+    wr = torch.from_numpy((rng.standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32)).to(dev)
+    lb = torch.from_numpy((rng.standard_normal(E) * 0.3).astype(np.float32)).to(dev) if logit_bias else None
+    sb = torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev) if select_bias else None
+    nb_in, nb_mid = q8k_blocks(hidden), q8k_blocks(ffn)
+
+    def bufs():
+        return dict(logits=torch.zeros((n_tok, E), **f32),
+                    xq=torch.zeros(n_tok * nb_in * 292, dtype=torch.uint8, device=dev),
+                    sel=torch.zeros((n_tok, k), dtype=torch.int32, device=dev),
+                    rw=torch.zeros((n_tok, k), **f32),
+                    ptrs=torch.zeros(n_tok * n_slots * 48, dtype=torch.uint8, device=dev),
+                    slot_w=torch.zeros((n_tok, n_slots), **f32),
+                    mid=torch.zeros((n_tok * n_slots, ffn), **f32),
+                    midq=torch.zeros(n_tok * n_slots * nb_mid * 292, dtype=torch.uint8, device=dev),
+                    out=torch.zeros((n_tok, hidden), **f32))
+
+    a = bufs()  # separate entry points
+    K.matmul_f32(a["logits"], wr, x, hidden, E, n_tok)
+    if lb is not None:
+        K.add_bias_rows(a["logits"], lb, E, n_tok)
+    zero = torch.zeros(E, **f32)
+    K.router_select(a["sel"], a["rw"], a["logits"], sb if sb is not None else zero, E, k, 1.25, n_tok, mode, 0)
+    K.moe_route_ptrs(a["ptrs"], a["slot_w"], a["sel"], a["rw"], bank, E, shared, n_tok, k)
+    K.quantize_q8_k(a["xq"], x, hidden, n_tok)
+    K.moe_pair_swiglu(a["mid"], a["ptrs"], a["slot_w"], a["xq"], hidden, ffn, n_slots, n_tok, L.grb, gq, act)
+    K.quantize_q8_k(a["midq"], a["mid"], ffn, n_tok * n_slots)
+    K.moe_down(a["out"], a["ptrs"], a["midq"], ffn, hidden, n_slots, n_tok, L.drb, dq)
+    if biases:
+        K.moe_down_bias(a["out"], a["ptrs"], a["slot_w"], hidden, n_slots, n_tok)
+
+    b = bufs()  # fused
+    K.router_logits_q8(b["logits"], b["xq"], x, wr, lb, hidden, E, n_tok)
+    K.moe_pair_routed(b["mid"], b["ptrs"], b["slot_w"], b["sel"], b["rw"], b["logits"], sb, E, k, 1.25, mode,
+                      bank, shared, b["xq"], hidden, ffn, n_tok, L.grb, gq, act)
+    K.moe_down_f32(b["out"], b["ptrs"], b["slot_w"], b["mid"], ffn, hidden, n_slots, n_tok, L.drb, dq, biases)
+    torch.cuda.synchronize()
+
+    for name in ("logits", "xq", "sel", "rw", "ptrs", "slot_w", "mid", "out"):
+        ga, gb = down(a[name]), down(b[name])
+        assert np.array_equal(ga.view(np.uint8), gb.view(np.uint8)), name
+    assert np.isfinite(down(b["out"])[: n_tok - 1]).all()
+
+
+def test_fused_error_contract(dev):
+    buf = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
+    bank = K.ExpertBank(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), None, None, None, 0, 0, 0, 0, 0, 0)
+    with pytest.raises(K.KernelError):  # softmax mode 2 (sink slots) is not fused
+        K.moe_pair_routed(buf, buf, buf, buf, buf, buf, None, 8, 2, 1.0, 2, bank, None, buf, 256, 256, 1, 144,
+                          QUANT_Q4_K, ACT_SILU)
+    with pytest.raises(K.KernelError):  # more than 64 slots
+        K.moe_pair_routed(buf, buf, buf, buf, buf, buf, None, 128, 65, 1.0, 1, bank, None, buf, 256, 256, 1, 144,
+                          QUANT_Q4_K, ACT_SILU)
+    with pytest.raises(K.KernelError):  # staged mid rows beyond 64 KiB
+        K.moe_down_f32(buf, buf, None, buf, 256 * 60, 256, 4, 1, 210 * 60, QUANT_Q6_K, False)
+    with pytest.raises(K.KernelError):  # bias without slot weights
+        K.moe_down_f32(buf, buf, None, buf, 256, 256, 4, 1, 210, QUANT_Q6_K, True)
+    with pytest.raises(K.KernelError):
+        K.router_logits_q8(buf, buf, buf, buf, None, 0, 8, 1)
+    torch.cuda.synchronize()
