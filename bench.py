@@ -419,7 +419,7 @@ def main():
                                                            warmup)
     layer_steps = max(20, steps // 2)
     for spec, path in ((synth.C3, "fused"), (synth.C4_Q2K, "grouped"), (synth.C4_IQ2, "grouped"),
-                       (synth.C5_B1, "fused"), (synth.C5_B64, "plain")):
+                       (synth.C5_B1, "fused"), (synth.C5_B64, "grouped")):
         if on(spec.name):
             results[spec.name] = bench_moe(ctx, spec, layer_steps, warmup, path)
         # the same layer through the reference's own (unfused) entry points

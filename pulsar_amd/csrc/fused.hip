@@ -133,8 +133,8 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
     float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
     float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
     if (row_ok && rg.holds_row()) {
-        if (p.gate_b) g += p.gate_b[row];
-        if (p.up_b) u += p.up_b[row];
+        if (p.gate_b) g += ldwf(p.gate_b + row);
+        if (p.up_b) u += ldwf(p.up_b + row);
         mid[so * mid_dim + row] = glu(g, u, act_op) * r.w;
     }
 }
@@ -212,7 +212,7 @@ __global__ __launch_bounds__(256) void moe_down_f32_kernel(
         if (add_bias) {
             float b = 0.0f;
             for (uint32_t s = 0; s < n_used; s++)
-                if (p_l[s].down_b) b += w_l[s] * p_l[s].down_b[row];
+                if (p_l[s].down_b) b += w_l[s] * ldwf(p_l[s].down_b + row);
             if (b != 0.0f) total += b;
         }
         out[(uint64_t)token * out_dim + row] = total;

@@ -15,6 +15,7 @@
 // Which 16 slots a lane group holds does not matter here: A and B hold the
 // same ones, and every sum below is over whole lane groups.
 #include "pk_rowdot.h"
+#include "pk_route.h"
 
 namespace pk {
 
@@ -240,6 +241,151 @@ int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_
     default:
         return -1;  // no MFMA kernel for this format: caller falls back
     }
+}
+
+// ------------------------------------------------- grouped MXFP4 (MoE) --
+// One block per (64-row block, expert group), 4 waves of 16 rows; the
+// group's (token, slot) pairs are taken 16 at a time, their q8_K rows staged
+// in LDS. Per 32-value block one v_mfma_i32_16x16x32_i8 gives the exact
+// block sums for 16 pairs x 16 rows: A = the pairs' q8 values, B = the rows'
+// E2M1 codes doubled to int8. Lane group kq holds values {0, 16, 8, 24}[kq]
+// + [0, 8) of the block: nibble kq & 1 of qs bytes 8 (kq >> 1) .. + 7.
+// Then, per (row, pair) and in block order, the reference's
+// sumf += scale_half(e) * sumi for sumi != 0 and, per 256 values,
+// row += yd * sumf (pulsar_kernels.cu:5715-5741).
+constexpr uint32_t kMmqPairs = 16;
+
+template <bool PAIR>
+__global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
+        float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
+        const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
+        const pulsar_block_q8_K *__restrict__ act, uint32_t k_dim, uint32_t k_blocks, uint32_t n_rows,
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t mmax) {
+    extern __shared__ __align__(16) uint8_t acts_lds[];  // mmax x k_blocks x kActLdsPitch
+    __shared__ uint32_t pr_l[kMmqPairs];
+    const uint32_t group = blockIdx.y;
+    const pulsar_expert_ptrs p = gptrs[group];
+    const uint8_t *w0 = PAIR ? (const uint8_t *)p.gate : (const uint8_t *)p.down;
+    const uint8_t *w1 = PAIR ? (const uint8_t *)p.up : nullptr;
+    if (!w0 || (PAIR && !w1)) return;
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    if (s0 >= s1) return;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t i = lane & 15u, kq = lane >> 4;
+    const uint32_t row = blockIdx.x * 64u + wave * 16u + i;  // this lane's B row
+    const uint32_t lrow = row < n_rows ? row : n_rows - 1u;
+    const uint8_t *rb0 = as_global(w0) + (uint64_t)lrow * row_bytes;  // block b: e at 17b, qs at 17b + 1
+    const uint8_t *rb1 = PAIR ? as_global(w1) + (uint64_t)lrow * row_bytes : nullptr;
+    const uint32_t q_off = 1u + 8u * (kq >> 1);
+    const uint32_t nsh = 4u * (kq & 1u);
+    const uint32_t a_off = 16u + 8u * (kq >> 1) + 16u * (kq & 1u);  // within an LDS q8 block, + 32 per block
+    const uint32_t nblk32 = k_dim / 32u;
+    const uint32_t act_bytes = k_blocks * kActLdsPitch;
+    for (uint32_t t0 = s0; t0 < s1; t0 += mmax) {
+        const uint32_t m = s1 - t0 < mmax ? s1 - t0 : mmax;
+        if (t0 != s0) __syncthreads();  // the previous tile's rows are consumed
+        const uint32_t per_row = k_blocks * 73u;
+        for (uint32_t k = threadIdx.x; k < m * per_row; k += blockDim.x) {
+            const uint32_t j = k / per_row, r = k - j * per_row;
+            const uint32_t sb = r / 73u, d = r - sb * 73u;
+            const uint32_t pr = pairs[t0 + j];
+            const uint64_t src_row = PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+            const uint32_t v = ld32((const uint8_t *)(act + src_row * k_blocks) + 4u * r);
+            *(uint32_t *)(acts_lds + j * act_bytes + sb * kActLdsPitch + act_lds_offset(d)) = v;
+        }
+        for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) pr_l[j] = pairs[t0 + j];
+        __syncthreads();
+        // A operand rows: pair i of the tile (zero when absent)
+        const bool a_ok = i < m;
+        const uint8_t *arow = acts_lds + (a_ok ? i : 0u) * act_bytes + a_off;
+        float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t sb = 0; sb < k_blocks; sb++) {
+            float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const uint32_t b0 = sb * 8u, nb = nblk32 - b0 < 8u ? nblk32 - b0 : 8u;
+            uint2 q0[8], q1[8];
+            uint32_t e0[8], e1[8];
+            uint2 a[8];
+#pragma unroll
+            for (uint32_t bl = 0; bl < 8; bl++) {
+                const uint32_t blk = b0 + (bl < nb ? bl : 0u);  // clamped: never past the row
+                q0[bl] = ldw64(rb0 + 17ull * blk + q_off);
+                e0[bl] = ldw8(rb0 + 17ull * blk);
+                if (PAIR) {
+                    q1[bl] = ldw64(rb1 + 17ull * blk + q_off);
+                    e1[bl] = ldw8(rb1 + 17ull * blk);
+                }
+                const uint2 av = *(const uint2 *)(arow + sb * kActLdsPitch + 32u * bl);
+                a[bl] = a_ok ? av : make_uint2(0u, 0u);
+            }
+#pragma unroll
+            for (uint32_t bl = 0; bl < 8; bl++) {
+                if (bl >= nb) break;  // uniform
+                const uint32_t lo = 0x0f0f0f0fu;
+                const uint2 c0 = make_uint2(mxfp4_kv4((q0[bl].x >> nsh) & lo), mxfp4_kv4((q0[bl].y >> nsh) & lo));
+                const v4i d0 = mfma16x16x32(a[bl], c0);
+                const float sc0 = mxfp4_scale_half(e0[bl]);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (d0[r] != 0) f0[r] += sc0 * (float)d0[r];
+                if (PAIR) {
+                    const uint2 c1 =
+                        make_uint2(mxfp4_kv4((q1[bl].x >> nsh) & lo), mxfp4_kv4((q1[bl].y >> nsh) & lo));
+                    const v4i d1 = mfma16x16x32(a[bl], c1);
+                    const float sc1 = mxfp4_scale_half(e1[bl]);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (d1[r] != 0) f1[r] += sc1 * (float)d1[r];
+                }
+            }
+            // yd of pairs 4kq + r at this super-block
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t pi = 4u * kq + r;
+                const float yd = pi < m ? *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch) : 0.0f;
+                acc0[r] += yd * f0[r];
+                if (PAIR) acc1[r] += yd * f1[r];
+            }
+        }
+        if (row < n_rows) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t pi = 4u * kq + r;
+                if (pi >= m) continue;
+                const uint32_t pr = pr_l[pi];
+                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+                if (PAIR) {
+                    float g = acc0[r], u = acc1[r];
+                    if (p.gate_b) g += ldwf(p.gate_b + row);
+                    if (p.up_b) u += ldwf(p.up_b + row);
+                    out[so * n_rows + row] = glu(g, u, act_op) * weights[so];
+                } else {
+                    out[so * n_rows + row] = acc0[r];
+                }
+            }
+        }
+    }
+}
+
+// Grouped MoE stages of MXFP4 experts on the matrix cores (pair: gate/up +
+// combine into mid; down: per-pair partials). Returns the launch status.
+int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const void *starts, const void *pairs,
+                             const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
+                             uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
+    const uint32_t k_blocks = (k_dim + 255u) / 256u;
+    const dim3 grid((n_rows + 63u) / 64u, n_group);
+    // pairs staged per round: up to 16, within 64 KiB of LDS
+    uint32_t mmax = 65536u / (k_blocks * kActLdsPitch);
+    mmax = mmax < 1u ? 1u : mmax > kMmqPairs ? kMmqPairs : mmax;
+    const size_t lds = (size_t)mmax * k_blocks * kActLdsPitch;
+    if (pair)
+        hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<true>, grid, dim3(256), lds, pk::stream(), out,
+                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
+                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op, mmax);
+    else
+        hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<false>, grid, dim3(256), lds, pk::stream(), out,
+                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
+                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op, mmax);
+    return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
 }
 
 }  // namespace pk

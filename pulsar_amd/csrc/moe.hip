@@ -56,8 +56,8 @@ __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
     if (row_ok && rg.holds_row()) {
         // bias on the projection output, then the combine, then the router
         // weight (pulsar_kernels.cu:2606-2612)
-        if (p.gate_b) g += p.gate_b[row];
-        if (p.up_b) u += p.up_b[row];
+        if (p.gate_b) g += ldwf(p.gate_b + row);
+        if (p.up_b) u += ldwf(p.up_b + row);
         mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
     }
 }
@@ -179,8 +179,8 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
             }
             const uint32_t row = pass * rpp + rg.rip;
             const bool row_ok = row < mid_dim;
-            const float gb = row_ok && p.gate_b ? p.gate_b[row] : 0.0f;
-            const float ub = row_ok && p.up_b ? p.up_b[row] : 0.0f;
+            const float gb = row_ok && p.gate_b ? ldwf(p.gate_b + row) : 0.0f;
+            const float ub = row_ok && p.up_b ? ldwf(p.up_b + row) : 0.0f;
             for (uint32_t j = 0; j < np; j++) {
                 const uint32_t pr = pr_l[j];
                 const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void down_bias_kernel(float *__restrict__ out,
     for (uint32_t s = 0; s < n_used; s++) {
         const uint64_t so = token * n_used + s;
         const float *db = ptrs[so].down_b;
-        if (db) b += weights[so] * db[row];
+        if (db) b += weights[so] * ldwf(db + row);
     }
     if (b != 0.0f) out[gid] += b;
 }
@@ -462,17 +462,33 @@ extern "C" int pulsar_moe_down(void *out, const void *ptrs, const void *midq, ui
 // Grouped entry points keep the reference's argument contract
 // (pulsar_kernels.cu:3488-3492, 3541-3547): in_dim (pair) and mid_dim (down)
 // multiples of 256, n_used <= 16 (4-bit slot field in `pairs`).
+namespace pk {
+// mmq.hip: the grouped stages of MXFP4 experts on the matrix cores
+int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const void *starts, const void *pairs,
+                             const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
+                             uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
+}  // namespace pk
+
 extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *starts,
                                               const void *pairs, const void *weights,
                                               const void *xq, uint32_t in_dim, uint32_t mid_dim,
                                               uint32_t n_used, uint32_t n_group,
                                               uint64_t row_bytes, uint32_t quant,
                                               uint32_t act_op) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    // MXFP4 rows need only whole 32-value blocks (a superset of the
+    // reference's in_dim % 256 contract, which keeps gpt-oss's 2880 off the
+    // grouped path, crates/engine/src/lib.rs:8354)
+    const uint32_t k_mult = quant == PULSAR_QUANT_MXFP4 ? 32u : 256u;
     if (!mid || !gptrs || !starts || !pairs || !weights || !xq || in_dim == 0 ||
-        in_dim % 256u != 0 || mid_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 ||
+        in_dim % k_mult != 0 || mid_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 ||
         n_group > 65535u || row_bytes == 0 ||
         (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI))
         return reject("moe pair swiglu grouped");
+    if (quant == PULSAR_QUANT_MXFP4)
+        return launch_grouped_mmq_mxfp4(true, (float *)mid, gptrs, starts, pairs, (const float *)weights,
+                                        (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group, row_bytes,
+                                        act_op);
     const Geo g = geo_for(quant, in_dim);
     PairGroupedLaunch f{mid, gptrs, starts, pairs, weights, xq, mid_dim, n_used, n_group, act_op, row_bytes, g};
     if (!quant_ok(quant)) return reject("moe pair swiglu grouped (quant)");
@@ -483,10 +499,16 @@ extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const v
                                        const void *pairs, const void *midq, uint32_t mid_dim,
                                        uint32_t out_dim, uint32_t n_used, uint32_t n_group,
                                        uint64_t row_bytes, uint32_t quant) {
-    if (!partial || !gptrs || !starts || !pairs || !midq || mid_dim == 0 || mid_dim % 256u != 0 ||
+    quant &= ~PULSAR_QUANT_A4_OK;
+    const uint32_t k_mult = quant == PULSAR_QUANT_MXFP4 ? 32u : 256u;
+    if (!partial || !gptrs || !starts || !pairs || !midq || mid_dim == 0 || mid_dim % k_mult != 0 ||
         out_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 || n_group > 65535u ||
         row_bytes == 0)
         return reject("moe down grouped");
+    if (quant == PULSAR_QUANT_MXFP4)
+        return launch_grouped_mmq_mxfp4(false, (float *)partial, gptrs, starts, pairs, nullptr,
+                                        (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
+                                        row_bytes, 0);
     const Geo g = geo_for(quant, mid_dim);
     DownGroupedLaunch f{partial, gptrs, starts, pairs, midq, out_dim, n_used, n_group, row_bytes, g};
     if (!quant_ok(quant)) return reject("moe down grouped (quant)");

@@ -77,23 +77,26 @@ PK_DEV uint4 ld128(const uint8_t *p) {
 }
 typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(1)));
 typedef uint32_t u32x2_u __attribute__((ext_vector_type(2), aligned(1)));
-// Streaming (read-once) weight loads: non-temporal hint, any alignment.
+typedef uint32_t u32_u __attribute__((aligned(1)));
+typedef uint16_t u16_u __attribute__((aligned(1)));
+#define PK_GLOBAL __attribute__((address_space(1)))
+// Weight loads, any alignment, always from global memory. Expert weight
+// pointers are read from pointer tables, so the compiler cannot infer their
+// address space: a generic (flat) load would also count against the LDS
+// wait counter and make LDS reads wait for HBM. The explicit global address
+// space keeps them plain global loads.
 PK_DEV uint4 ldw128(const uint8_t *p) {
-#ifdef PK_NT_LOADS
-    const u32x4_u v = __builtin_nontemporal_load((const u32x4_u *)p);
+    const u32x4_u v = *(const PK_GLOBAL u32x4_u *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
-#else
-    return ld128(p);
-#endif
 }
 PK_DEV uint2 ldw64(const uint8_t *p) {
-#ifdef PK_NT_LOADS
-    const u32x2_u v = __builtin_nontemporal_load((const u32x2_u *)p);
+    const u32x2_u v = *(const PK_GLOBAL u32x2_u *)p;
     return make_uint2(v.x, v.y);
-#else
-    return ld64(p);
-#endif
 }
+PK_DEV uint32_t ldw32(const uint8_t *p) { return *(const PK_GLOBAL u32_u *)p; }
+PK_DEV uint16_t ldw16(const uint8_t *p) { return *(const PK_GLOBAL u16_u *)p; }
+PK_DEV uint32_t ldw8(const uint8_t *p) { return *(const PK_GLOBAL uint8_t *)p; }
+PK_DEV float ldwf(const float *p) { return *(const PK_GLOBAL float *)p; }
 PK_DEV uint16_t ld16(const uint8_t *p) {
     uint16_t v;
     __builtin_memcpy(&v, p, 2);

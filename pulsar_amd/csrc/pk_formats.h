@@ -210,7 +210,7 @@ struct Fmt<PULSAR_QUANT_Q6_K> {
         w.lb = ldw128(blk + 64u * h + 32u + 16u * k);
         w.qh = ldw128(blk + 128u + 32u * h + 16u * k);
         w.sc = ldw64(blk + 192u + 8u * h);
-        w.d = ld16(blk + 208u);
+        w.d = ldw16(blk + 208u);
         return w;
     }
     PK_DEV static Part part(const W &w, const Act &a, uint32_t u, const uint2 *) {
@@ -269,7 +269,7 @@ struct Fmt<PULSAR_QUANT_Q2_K> {
         W w;
         w.qs = ldw128(blk + 16u + 32u * k + 16u * half);
         w.sc = ldw64(blk + 8u * k);
-        w.dd = ld32(blk + 80u);
+        w.dd = ldw32(blk + 80u);
         return w;
     }
     PK_DEV static Part part(const W &w, const Act &a, uint32_t u, const uint2 *) {
@@ -326,7 +326,7 @@ struct Fmt<PULSAR_QUANT_IQ2_XXS> {
         const uint8_t *blk = row + (uint64_t)(g >> 2) * kSbBytes;
         W w;
         w.aux = ldw128(blk + 2u + 16u * (g & 3u));
-        w.d = ld16(blk);
+        w.d = ldw16(blk);
         return w;
     }
     PK_DEV static int32_t group(const uint2 *lut, uint32_t aux0, uint32_t aux1, uint4 a0, uint4 a1) {
@@ -415,7 +415,7 @@ struct Fmt<PULSAR_QUANT_MXFP4> {
         const uint8_t *p1 = w.two ? p + 17 : p;
         w.q0 = ldw128(p + 1);
         w.q1 = ldw128(p1 + 1);
-        w.e = (uint32_t)p[0] | ((w.two ? (uint32_t)p1[0] : 0u) << 8);
+        w.e = ldw8(p) | ((w.two ? ldw8(p1) : 0u) << 8);
         return w;
     }
     // sumf += scale_half(e) * sumi for each block with sumi != 0, in block order

@@ -181,14 +181,44 @@ def test_grouped_matches_plain_and_oracle(dev, gq):
     assert np.array_equal(down(out), acc)
 
 
+@pytest.mark.parametrize("n_tok", [3, 40])
+def test_grouped_mxfp4_mfma(dev, n_tok):
+    """MXFP4 groups run on the matrix cores (more than 16 pairs per group at
+    n_tok 40: two pair tiles); tail super-blocks (576 = 2 x 256 + 64, 320 =
+    256 + 64), biases, swiglu_oai and NULL slots."""
+    L = Layer(QUANT_MXFP4, QUANT_MXFP4, hidden=576, ffn=320, E=6, n_used=4, n_tok=n_tok, biases=True,
+              null_slots=(1, 6))
+    hptrs, dptrs, xq, want_mid, midq, want_out = check_pair_down(L, ACT_SWIGLU_OAI)
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu_grouped(mid, gptrs, up(starts), up(pairs), up_f32(L.w), up(xq), L.hidden, L.ffn,
+                              L.n_used, len(ids), L.grb, QUANT_MXFP4, ACT_SWIGLU_OAI)
+    got_mid = down(mid)
+    bound = pair_bound(L, xq, ACT_SWIGLU_OAI) + 4e-7 * np.abs(want_mid) + 1e-30
+    err = np.abs(got_mid.astype(np.float64) - want_mid)
+    assert (err <= bound).all(), f"grouped mfma pair: max err {err.max():.3e}"
+    partial = zeros_f32((L.n_tok * L.n_used, L.hidden))
+    K.moe_down_grouped(partial, gptrs, up(starts), up(pairs), up(midq), L.ffn, L.hidden, L.n_used, len(ids),
+                       L.drb, QUANT_MXFP4)
+    out = zeros_f32((L.n_tok, L.hidden))
+    K.moe_slot_sum(out, partial, L.hidden, L.n_used, L.n_tok)
+    # the down bias is a separate stage on both paths
+    want = oracle.moe_down(hptrs, midq, L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, QUANT_MXFP4)
+    err = np.abs(down(out).astype(np.float64) - want)
+    assert (err <= down_bound(L, midq)).all(), f"grouped mfma down: max err {err.max():.3e}"
+
+
 def test_grouped_contract(dev):
     buf = up(np.zeros(4096, np.uint8))
     with pytest.raises(K.KernelError):  # in_dim % 256 (pulsar_kernels.cu:3488)
-        K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 2880, 64, 4, 1, 1530, QUANT_MXFP4, 0)
+        K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 2880, 64, 4, 1, 1530, QUANT_Q4_K, 0)
+    with pytest.raises(K.KernelError):  # MXFP4: whole 32-value blocks
+        K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 2870, 64, 4, 1, 1530, QUANT_MXFP4, 0)
     with pytest.raises(K.KernelError):  # n_used > 16 cannot be packed in pairs
         K.moe_pair_swiglu_grouped(buf, buf, buf, buf, buf, buf, 256, 64, 17, 1, 144, QUANT_Q4_K, 0)
     with pytest.raises(K.KernelError):  # mid_dim % 256 for the grouped down
-        K.moe_down_grouped(buf, buf, buf, buf, buf, 704, 64, 4, 1, 374, QUANT_MXFP4)
+        K.moe_down_grouped(buf, buf, buf, buf, buf, 704, 64, 4, 1, 374, QUANT_Q6_K)
     with pytest.raises(K.KernelError):
         K.moe_pair_swiglu(buf, buf, buf, buf, 256, 64, 4, 1, 144, 99, 0)  # unknown quant
     torch.cuda.synchronize()
