@@ -284,16 +284,13 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
     for (uint32_t t0 = s0; t0 < s1; t0 += mmax) {
         const uint32_t m = s1 - t0 < mmax ? s1 - t0 : mmax;
         if (t0 != s0) __syncthreads();  // the previous tile's rows are consumed
-        const uint32_t per_row = k_blocks * 73u;
-        for (uint32_t k = threadIdx.x; k < m * per_row; k += blockDim.x) {
-            const uint32_t j = k / per_row, r = k - j * per_row;
-            const uint32_t sb = r / 73u, d = r - sb * 73u;
-            const uint32_t pr = pairs[t0 + j];
-            const uint64_t src_row = PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-            const uint32_t v = ld32((const uint8_t *)(act + src_row * k_blocks) + 4u * r);
-            *(uint32_t *)(acts_lds + j * act_bytes + sb * kActLdsPitch + act_lds_offset(d)) = v;
-        }
         for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) pr_l[j] = pairs[t0 + j];
+        __syncthreads();
+        stage_q8_rows<8>(acts_lds, m, k_blocks, [&](uint32_t j) {
+            const uint32_t pr = pr_l[j];
+            const uint64_t src_row = PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+            return act + src_row * k_blocks;
+        });
         __syncthreads();
         // A operand rows: pair i of the tile (zero when absent)
         const bool a_ok = i < m;

@@ -113,19 +113,18 @@ constexpr uint32_t kGrpMaxPairs = 16u;   // pairs staged per round
 // Copies the q8_K rows of pairs [c0, c0 + np) into LDS (load_act_lds
 // layout, `blocks` super-blocks per row) and their pair ids into pr_l.
 // DOWN: the row is the (token, slot)'s mid row, else the token's row.
+// Ends with a block barrier.
 template <bool DOWN>
 PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const uint32_t *pairs, uint32_t c0, uint32_t np,
                             const pulsar_block_q8_K *src, uint32_t blocks, uint32_t n_used) {
-    const uint32_t per_row = blocks * 73u;  // dwords per q8_K row
-    for (uint32_t k = threadIdx.x; k < np * per_row; k += blockDim.x) {
-        const uint32_t j = k / per_row, r = k - j * per_row;
-        const uint32_t sb = r / 73u, d = r - sb * 73u;
-        const uint32_t pr = pairs[c0 + j];
-        const uint64_t row = DOWN ? (uint64_t)(pr >> 4) * n_used + (pr & 15u) : (uint64_t)(pr >> 4);
-        const uint32_t v = ld32((const uint8_t *)(src + row * blocks) + 4u * r);
-        *(uint32_t *)(acts + j * blocks * kActLdsPitch + sb * kActLdsPitch + act_lds_offset(d)) = v;
-    }
     for (uint32_t j = threadIdx.x; j < np; j += blockDim.x) pr_l[j] = pairs[c0 + j];
+    __syncthreads();
+    stage_q8_rows<2>(acts, np, blocks, [&](uint32_t j) {
+        const uint32_t pr = pr_l[j];
+        const uint64_t row = DOWN ? (uint64_t)(pr >> 4) * n_used + (pr & 15u) : (uint64_t)(pr >> 4);
+        return src + row * blocks;
+    });
+    __syncthreads();
 }
 
 // Grouped kernels: one block per (row block, expert group). The group's
@@ -167,7 +166,6 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
             load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)row_of(pass0) * row_bytes, rg, wu);
         }
         stage_pair_acts<false>(acts_lds, pr_l, pairs, c0, np, xq, in_blocks, n_used);
-        __syncthreads();
         for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
             const uint32_t pass = pass0 + k;
             if (pass >= n_pass) break;  // wave-uniform
@@ -243,7 +241,6 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
             load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)row_of(pass0) * row_bytes, rg, w);
         }
         stage_pair_acts<true>(acts_lds, pr_l, pairs, c0, np, midq, mid_blocks, n_used);
-        __syncthreads();
         for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
             const uint32_t pass = pass0 + k;
             if (pass >= n_pass) break;  // wave-uniform
