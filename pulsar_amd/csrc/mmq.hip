@@ -244,24 +244,34 @@ int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_
 }
 
 // ------------------------------------------------- grouped MXFP4 (MoE) --
-// One block per (64-row block, expert group), 4 waves of 16 rows; the
-// group's (token, slot) pairs are taken 16 at a time, their q8_K rows staged
-// in LDS. Per 32-value block one v_mfma_i32_16x16x32_i8 gives the exact
-// block sums for 16 pairs x 16 rows: A = the pairs' q8 values, B = the rows'
-// E2M1 codes doubled to int8. Lane group kq holds values {0, 16, 8, 24}[kq]
-// + [0, 8) of the block: nibble kq & 1 of qs bytes 8 (kq >> 1) .. + 7.
-// Then, per (row, pair) and in block order, the reference's
-// sumf += scale_half(e) * sumi for sumi != 0 and, per 256 values,
-// row += yd * sumf (pulsar_kernels.cu:5715-5741).
+// One block per (16-row tile, expert group); the group's (token, slot)
+// pairs are taken 16 at a time. Per 32-value block one
+// v_mfma_i32_16x16x32_i8 gives the exact block sums for 16 pairs x 16 rows:
+// A = the pairs' q8 values (read from their q8_K rows, which stay in cache
+// across the group's row tiles), B = the rows' E2M1 codes doubled to int8.
+// Lane group kq holds values {0, 16, 8, 24}[kq] + [0, 8) of the block:
+// nibble kq & 1 of qs bytes 8 (kq >> 1) .. + 7. The 4 waves split the row's
+// super-blocks (wave w: w, w + 4, ...). A wave first copies its super-block
+// of the 16 rows into its own LDS area, one 17-byte block per lane (a
+// wave-wide load covers 8 rows x 136 contiguous bytes), with qs at 16-byte
+// aligned slots and e apart; the MFMA operands are then aligned LDS reads.
+// Per (row, pair) a wave forms the
+// reference's super-block value yd * sumf, sumf += scale_half(e) * sumi in
+// block order for sumi != 0 (pulsar_kernels.cu:5715-5741), into LDS, and
+// the block adds the super-blocks in order.
 constexpr uint32_t kMmqPairs = 16;
+constexpr uint32_t kMmqMaxSb = 32;  // super-blocks per row (in_dim <= 8192)
 
 template <bool PAIR>
 __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
         float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
         const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
         const pulsar_block_q8_K *__restrict__ act, uint32_t k_dim, uint32_t k_blocks, uint32_t n_rows,
-        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t mmax) {
-    extern __shared__ __align__(16) uint8_t acts_lds[];  // mmax x k_blocks x kActLdsPitch
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op) {
+    // [PAIR ? 2 : 1][k_blocks][16 rows][17] super-block values
+    extern __shared__ __align__(16) float sbval[];
+    __shared__ __align__(16) uint4 wq_l[4][PAIR ? 2 : 1][16][8];  // [wave][matrix][row][block] qs
+    __shared__ __align__(8) uint8_t we_l[4][PAIR ? 2 : 1][16][8];  // e
     __shared__ uint32_t pr_l[kMmqPairs];
     const uint32_t group = blockIdx.y;
     const pulsar_expert_ptrs p = gptrs[group];
@@ -272,48 +282,85 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
     if (s0 >= s1) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
-    const uint32_t row = blockIdx.x * 64u + wave * 16u + i;  // this lane's B row
-    const uint32_t lrow = row < n_rows ? row : n_rows - 1u;
-    const uint8_t *rb0 = as_global(w0) + (uint64_t)lrow * row_bytes;  // block b: e at 17b, qs at 17b + 1
-    const uint8_t *rb1 = PAIR ? as_global(w1) + (uint64_t)lrow * row_bytes : nullptr;
-    const uint32_t q_off = 1u + 8u * (kq >> 1);
+    const uint32_t row0 = blockIdx.x * 16u;
+    // copy lanes: block lane & 7 of rows lane >> 3 and 8 + (lane >> 3)
+    const uint32_t cb = lane & 7u, cr = lane >> 3;
+    const uint8_t *cp0[2], *cp1[2];  // block b of the row: e at 17b, qs at 17b + 1
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+        const uint32_t r = row0 + cr + 8u * h;
+        const uint64_t ro = (uint64_t)(r < n_rows ? r : n_rows - 1u) * row_bytes;
+        cp0[h] = as_global(w0) + ro;
+        cp1[h] = PAIR ? as_global(w1) + ro : nullptr;
+    }
     const uint32_t nsh = 4u * (kq & 1u);
-    const uint32_t a_off = 16u + 8u * (kq >> 1) + 16u * (kq & 1u);  // within an LDS q8 block, + 32 per block
+    const uint32_t a_off = 4u + 8u * (kq >> 1) + 16u * (kq & 1u);  // within a q8_K block, + 32 per 32-block
     const uint32_t nblk32 = k_dim / 32u;
-    const uint32_t act_bytes = k_blocks * kActLdsPitch;
-    for (uint32_t t0 = s0; t0 < s1; t0 += mmax) {
-        const uint32_t m = s1 - t0 < mmax ? s1 - t0 : mmax;
-        if (t0 != s0) __syncthreads();  // the previous tile's rows are consumed
-        for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) pr_l[j] = pairs[t0 + j];
+    const uint32_t sv_stride = 16u * 17u;  // one super-block's [16 rows][17]
+    for (uint32_t t0 = s0; t0 < s1; t0 += kMmqPairs) {
+        const uint32_t m = s1 - t0 < kMmqPairs ? s1 - t0 : kMmqPairs;
+        if (t0 != s0) __syncthreads();  // the previous tile's values are consumed
+        if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
         __syncthreads();
-        stage_q8_rows<8>(acts_lds, m, k_blocks, [&](uint32_t j) {
-            const uint32_t pr = pr_l[j];
-            const uint64_t src_row = PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-            return act + src_row * k_blocks;
-        });
-        __syncthreads();
-        // A operand rows: pair i of the tile (zero when absent)
+        // A operand: pair i of the tile (zero when absent); D elements: pairs 4kq + r
         const bool a_ok = i < m;
-        const uint8_t *arow = acts_lds + (a_ok ? i : 0u) * act_bytes + a_off;
-        float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t sb = 0; sb < k_blocks; sb++) {
+        const uint32_t pa = pr_l[a_ok ? i : 0u];
+        const uint8_t *arow =
+            (const uint8_t *)(act + (PAIR ? (uint64_t)(pa >> 4) : (uint64_t)(pa >> 4) * n_used + (pa & 15u)) *
+                                        k_blocks);
+        const uint8_t *drow[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t pi = 4u * kq + r;
+            const uint32_t pr = pr_l[pi < m ? pi : 0u];
+            drow[r] = (const uint8_t *)(act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) *
+                                                  k_blocks);
+        }
+        for (uint32_t sb = wave; sb < k_blocks; sb += 4u) {
             float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
             const uint32_t b0 = sb * 8u, nb = nblk32 - b0 < 8u ? nblk32 - b0 : 8u;
-            uint2 q0[8], q1[8];
-            uint32_t e0[8], e1[8];
+            // copy the super-block's 16 rows (clamped: never past the row)
+            const uint64_t co = 17ull * (b0 + (cb < nb ? cb : 0u));
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                const uint4 q = ldw128(cp0[h] + co + 1u);
+                const uint32_t e = ldw8(cp0[h] + co);
+                wq_l[wave][0][cr + 8u * h][cb] = q;
+                we_l[wave][0][cr + 8u * h][cb] = (uint8_t)e;
+                if (PAIR) {
+                    const uint4 q1v = ldw128(cp1[h] + co + 1u);
+                    const uint32_t e1v = ldw8(cp1[h] + co);
+                    wq_l[wave][PAIR ? 1 : 0][cr + 8u * h][cb] = q1v;
+                    we_l[wave][PAIR ? 1 : 0][cr + 8u * h][cb] = (uint8_t)e1v;
+                }
+            }
             uint2 a[8];
 #pragma unroll
             for (uint32_t bl = 0; bl < 8; bl++) {
-                const uint32_t blk = b0 + (bl < nb ? bl : 0u);  // clamped: never past the row
-                q0[bl] = ldw64(rb0 + 17ull * blk + q_off);
-                e0[bl] = ldw8(rb0 + 17ull * blk);
-                if (PAIR) {
-                    q1[bl] = ldw64(rb1 + 17ull * blk + q_off);
-                    e1[bl] = ldw8(rb1 + 17ull * blk);
-                }
-                const uint2 av = *(const uint2 *)(arow + sb * kActLdsPitch + 32u * bl);
+                const uint2 av = ld64(arow + (uint64_t)sb * 292u + a_off + 32u * bl);
                 a[bl] = a_ok ? av : make_uint2(0u, 0u);
             }
+            // the wave's own LDS area: visible to the wave's other lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint2 q0[8], q1[8];
+            uint32_t e0[8], e1[8];
+            const uint2 ev0 = *(const uint2 *)&we_l[wave][0][i][0];
+            const uint2 ev1 = *(const uint2 *)&we_l[wave][PAIR ? 1 : 0][i][0];
+#pragma unroll
+            for (uint32_t bl = 0; bl < 8; bl++) {
+                q0[bl] = *((const uint2 *)&wq_l[wave][0][i][bl] + (kq >> 1));
+                e0[bl] = byte_of(ev0, bl);
+                if (PAIR) {
+                    q1[bl] = *((const uint2 *)&wq_l[wave][PAIR ? 1 : 0][i][bl] + (kq >> 1));
+                    e1[bl] = byte_of(ev1, bl);
+                }
+            }
+            float yd[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                yd[r] = __builtin_bit_cast(float, ld32(drow[r] + (uint64_t)sb * 292u));
 #pragma unroll
             for (uint32_t bl = 0; bl < 8; bl++) {
                 if (bl >= nb) break;  // uniform
@@ -334,30 +381,30 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
                         if (d1[r] != 0) f1[r] += sc1 * (float)d1[r];
                 }
             }
-            // yd of pairs 4kq + r at this super-block
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint32_t pi = 4u * kq + r;
-                const float yd = pi < m ? *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch) : 0.0f;
-                acc0[r] += yd * f0[r];
-                if (PAIR) acc1[r] += yd * f1[r];
+                sbval[sb * sv_stride + i * 17u + 4u * kq + r] = yd[r] * f0[r];
+                if (PAIR) sbval[(k_blocks + sb) * sv_stride + i * 17u + 4u * kq + r] = yd[r] * f1[r];
             }
         }
-        if (row < n_rows) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t pi = 4u * kq + r;
-                if (pi >= m) continue;
-                const uint32_t pr = pr_l[pi];
-                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-                if (PAIR) {
-                    float g = acc0[r], u = acc1[r];
-                    if (p.gate_b) g += ldwf(p.gate_b + row);
-                    if (p.up_b) u += ldwf(p.up_b + row);
-                    out[so * n_rows + row] = glu(g, u, act_op) * weights[so];
-                } else {
-                    out[so * n_rows + row] = acc0[r];
-                }
+        __syncthreads();
+        // one thread per (row, pair): the super-blocks in order, then the epilogue
+        const uint32_t ri = threadIdx.x & 15u, pi = threadIdx.x >> 4;
+        if (pi < m && row0 + ri < n_rows) {
+            float g = 0.0f, u = 0.0f;
+            for (uint32_t sb = 0; sb < k_blocks; sb++) {
+                g += sbval[sb * sv_stride + ri * 17u + pi];
+                if (PAIR) u += sbval[(k_blocks + sb) * sv_stride + ri * 17u + pi];
+            }
+            const uint32_t pr = pr_l[pi];
+            const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+            const uint32_t orow = row0 + ri;
+            if (PAIR) {
+                if (p.gate_b) g += ldwf(p.gate_b + orow);
+                if (p.up_b) u += ldwf(p.up_b + orow);
+                out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
+            } else {
+                out[so * n_rows + orow] = g;
             }
         }
     }
@@ -369,19 +416,17 @@ int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const voi
                              const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
                              uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
     const uint32_t k_blocks = (k_dim + 255u) / 256u;
-    const dim3 grid((n_rows + 63u) / 64u, n_group);
-    // pairs staged per round: up to 16, within 64 KiB of LDS
-    uint32_t mmax = 65536u / (k_blocks * kActLdsPitch);
-    mmax = mmax < 1u ? 1u : mmax > kMmqPairs ? kMmqPairs : mmax;
-    const size_t lds = (size_t)mmax * k_blocks * kActLdsPitch;
+    if (k_blocks > kMmqMaxSb) return reject("moe grouped mxfp4 (row width above 8192)");
+    const dim3 grid((n_rows + 15u) / 16u, n_group);
+    const size_t lds = (size_t)(pair ? 2u : 1u) * k_blocks * 16u * 17u * sizeof(float);
     if (pair)
         hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<true>, grid, dim3(256), lds, pk::stream(), out,
                            (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
-                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op, mmax);
+                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op);
     else
         hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<false>, grid, dim3(256), lds, pk::stream(), out,
                            (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
-                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op, mmax);
+                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op);
     return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
 }
 
