@@ -247,20 +247,19 @@ int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_
 // One block per (16-row tile, expert group); the group's (token, slot)
 // pairs are taken 16 at a time. Per 32-value block one
 // v_mfma_i32_16x16x32_i8 gives the exact block sums for 16 pairs x 16 rows:
-// A = the pairs' q8 values (read from their q8_K rows, which stay in cache
-// across the group's row tiles), B = the rows' E2M1 codes doubled to int8.
-// Lane group kq holds values {0, 16, 8, 24}[kq] + [0, 8) of the block:
-// nibble kq & 1 of qs bytes 8 (kq >> 1) .. + 7. The 4 waves split the row's
-// super-blocks (wave w: w, w + 4, ...). A wave first copies its super-block
-// of the 16 rows into its own LDS area, one 17-byte block per lane (a
-// wave-wide load covers 8 rows x 136 contiguous bytes), with qs at 16-byte
-// aligned slots and e apart; the MFMA operands are then aligned LDS reads.
-// Per (row, pair) a wave forms the
-// reference's super-block value yd * sumf, sumf += scale_half(e) * sumi in
-// block order for sumi != 0 (pulsar_kernels.cu:5715-5741), into LDS, and
-// the block adds the super-blocks in order.
+// A = the pairs' q8 values, B = the rows' E2M1 codes doubled to int8. Lane
+// group kq holds values {0, 16, 8, 24}[kq] + [0, 8) of the block: nibble
+// kq & 1 of qs bytes 8 (kq >> 1) .. + 7. The 4 waves take contiguous ranges
+// of the row's super-blocks. Per super-block a wave copies the 16 rows'
+// blocks (one 17-byte block per lane: a wave-wide load covers 8 rows x 136
+// contiguous bytes; qs to 16-byte aligned slots, e apart) and the 16 pairs'
+// q8 values (a wave-wide load covers 4 pairs x 256 bytes) into its own LDS
+// area, so every global load is contiguous and every MFMA operand is an
+// aligned LDS read. Per (row, pair) and in block order the reference's
+// sumf += scale_half(e) * sumi for sumi != 0, then row += yd * sumf per
+// super-block (pulsar_kernels.cu:5715-5741) in the wave's range; the
+// block adds the 4 ranges in order.
 constexpr uint32_t kMmqPairs = 16;
-constexpr uint32_t kMmqMaxSb = 32;  // super-blocks per row (in_dim <= 8192)
 
 template <bool PAIR>
 __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
@@ -268,10 +267,13 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
         const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
         const pulsar_block_q8_K *__restrict__ act, uint32_t k_dim, uint32_t k_blocks, uint32_t n_rows,
         uint32_t n_used, uint64_t row_bytes, uint32_t act_op) {
-    // [PAIR ? 2 : 1][k_blocks][16 rows][17] super-block values
-    extern __shared__ __align__(16) float sbval[];
-    __shared__ __align__(16) uint4 wq_l[4][PAIR ? 2 : 1][16][8];  // [wave][matrix][row][block] qs
-    __shared__ __align__(8) uint8_t we_l[4][PAIR ? 2 : 1][16][8];  // e
+    constexpr uint32_t NM = PAIR ? 2 : 1;
+    // rows / pairs padded by 16 bytes: the 16 rows (pairs) an MFMA operand
+    // read touches fall in distinct LDS banks
+    __shared__ __align__(16) uint4 wq_l[4][NM][16][9];    // [wave][matrix][row][block] qs
+    __shared__ __align__(8) uint8_t we_l[4][NM][16][8];   // e
+    __shared__ __align__(16) uint4 aq_l[4][16][17];       // [wave][pair][16-byte piece] q8 values
+    __shared__ float part[4][NM][16][17];                 // [wave][matrix][row][pair]
     __shared__ uint32_t pr_l[kMmqPairs];
     const uint32_t group = blockIdx.y;
     const pulsar_expert_ptrs p = gptrs[group];
@@ -283,32 +285,36 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
     const uint32_t row0 = blockIdx.x * 16u;
-    // copy lanes: block lane & 7 of rows lane >> 3 and 8 + (lane >> 3)
+    // weight copy lanes: block lane & 7 of rows lane >> 3 and 8 + (lane >> 3)
     const uint32_t cb = lane & 7u, cr = lane >> 3;
-    const uint8_t *cp0[2], *cp1[2];  // block b of the row: e at 17b, qs at 17b + 1
+    const uint8_t *cp[NM][2];  // block b of the row: e at 17b, qs at 17b + 1
 #pragma unroll
     for (uint32_t h = 0; h < 2; h++) {
         const uint32_t r = row0 + cr + 8u * h;
         const uint64_t ro = (uint64_t)(r < n_rows ? r : n_rows - 1u) * row_bytes;
-        cp0[h] = as_global(w0) + ro;
-        cp1[h] = PAIR ? as_global(w1) + ro : nullptr;
+        cp[0][h] = as_global(w0) + ro;
+        if (PAIR) cp[NM - 1][h] = as_global(w1) + ro;
     }
     const uint32_t nsh = 4u * (kq & 1u);
-    const uint32_t a_off = 4u + 8u * (kq >> 1) + 16u * (kq & 1u);  // within a q8_K block, + 32 per 32-block
+    const uint32_t a_piece = (kq >> 1) + 2u * (kq & 1u);  // 8-byte piece of a 32-value block: 0, 2, 1, 3
     const uint32_t nblk32 = k_dim / 32u;
-    const uint32_t sv_stride = 16u * 17u;  // one super-block's [16 rows][17]
+    const uint32_t per = (k_blocks + 3u) / 4u;
+    const uint32_t sb_lo = wave * per, sb_hi = sb_lo + per < k_blocks ? sb_lo + per : k_blocks;
     for (uint32_t t0 = s0; t0 < s1; t0 += kMmqPairs) {
         const uint32_t m = s1 - t0 < kMmqPairs ? s1 - t0 : kMmqPairs;
-        if (t0 != s0) __syncthreads();  // the previous tile's values are consumed
+        if (t0 != s0) __syncthreads();  // the previous tile's partials are consumed
         if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
         __syncthreads();
-        // A operand: pair i of the tile (zero when absent); D elements: pairs 4kq + r
-        const bool a_ok = i < m;
-        const uint32_t pa = pr_l[a_ok ? i : 0u];
-        const uint8_t *arow =
-            (const uint8_t *)(act + (PAIR ? (uint64_t)(pa >> 4) : (uint64_t)(pa >> 4) * n_used + (pa & 15u)) *
-                                        k_blocks);
-        const uint8_t *drow[4];
+        // activation copy lanes: piece lane & 15 of pairs lane >> 4 + 4j
+        const uint8_t *ap[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const uint32_t pi = (lane >> 4) + 4u * j;
+            const uint32_t pr = pr_l[pi < m ? pi : 0u];
+            ap[j] = (const uint8_t *)(act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) *
+                                                k_blocks) + 4u + 16u * (lane & 15u);
+        }
+        const uint8_t *drow[4];  // yd of pairs 4kq + r
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const uint32_t pi = 4u * kq + r;
@@ -316,93 +322,97 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
             drow[r] = (const uint8_t *)(act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) *
                                                   k_blocks);
         }
-        for (uint32_t sb = wave; sb < k_blocks; sb += 4u) {
-            float f0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, f1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float acc[NM][4];
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
+        for (uint32_t sb = sb_lo; sb < sb_hi; sb++) {
             const uint32_t b0 = sb * 8u, nb = nblk32 - b0 < 8u ? nblk32 - b0 : 8u;
             // copy the super-block's 16 rows (clamped: never past the row)
             const uint64_t co = 17ull * (b0 + (cb < nb ? cb : 0u));
+            uint4 q[NM][2];
+            uint32_t e[NM][2];
 #pragma unroll
-            for (uint32_t h = 0; h < 2; h++) {
-                const uint4 q = ldw128(cp0[h] + co + 1u);
-                const uint32_t e = ldw8(cp0[h] + co);
-                wq_l[wave][0][cr + 8u * h][cb] = q;
-                we_l[wave][0][cr + 8u * h][cb] = (uint8_t)e;
-                if (PAIR) {
-                    const uint4 q1v = ldw128(cp1[h] + co + 1u);
-                    const uint32_t e1v = ldw8(cp1[h] + co);
-                    wq_l[wave][PAIR ? 1 : 0][cr + 8u * h][cb] = q1v;
-                    we_l[wave][PAIR ? 1 : 0][cr + 8u * h][cb] = (uint8_t)e1v;
+            for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+                for (uint32_t h = 0; h < 2; h++) {
+                    q[mt][h] = ldw128(cp[mt][h] + co + 1u);
+                    e[mt][h] = ldw8(cp[mt][h] + co);
                 }
-            }
-            uint2 a[8];
+            uint4 av[4];
 #pragma unroll
-            for (uint32_t bl = 0; bl < 8; bl++) {
-                const uint2 av = ld64(arow + (uint64_t)sb * 292u + a_off + 32u * bl);
-                a[bl] = a_ok ? av : make_uint2(0u, 0u);
+            for (uint32_t j = 0; j < 4; j++) av[j] = ld128(ap[j] + (uint64_t)sb * 292u);
+            float yd[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) yd[r] = __builtin_bit_cast(float, ld32(drow[r] + (uint64_t)sb * 292u));
+#pragma unroll
+            for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+                for (uint32_t h = 0; h < 2; h++) {
+                    wq_l[wave][mt][cr + 8u * h][cb] = q[mt][h];
+                    we_l[wave][mt][cr + 8u * h][cb] = (uint8_t)e[mt][h];
+                }
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t pi = (lane >> 4) + 4u * j;
+                aq_l[wave][pi][lane & 15u] = pi < m ? av[j] : make_uint4(0u, 0u, 0u, 0u);
             }
             // the wave's own LDS area: visible to the wave's other lanes
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            uint2 q0[8], q1[8];
-            uint32_t e0[8], e1[8];
-            const uint2 ev0 = *(const uint2 *)&we_l[wave][0][i][0];
-            const uint2 ev1 = *(const uint2 *)&we_l[wave][PAIR ? 1 : 0][i][0];
+            float f[NM][4];
 #pragma unroll
-            for (uint32_t bl = 0; bl < 8; bl++) {
-                q0[bl] = *((const uint2 *)&wq_l[wave][0][i][bl] + (kq >> 1));
-                e0[bl] = byte_of(ev0, bl);
-                if (PAIR) {
-                    q1[bl] = *((const uint2 *)&wq_l[wave][PAIR ? 1 : 0][i][bl] + (kq >> 1));
-                    e1[bl] = byte_of(ev1, bl);
-                }
-            }
-            float yd[4];
+            for (uint32_t mt = 0; mt < NM; mt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                yd[r] = __builtin_bit_cast(float, ld32(drow[r] + (uint64_t)sb * 292u));
+                for (int r = 0; r < 4; r++) f[mt][r] = 0.0f;
+            uint2 ev[NM];
+#pragma unroll
+            for (uint32_t mt = 0; mt < NM; mt++) ev[mt] = *(const uint2 *)&we_l[wave][mt][i][0];
 #pragma unroll
             for (uint32_t bl = 0; bl < 8; bl++) {
                 if (bl >= nb) break;  // uniform
-                const uint32_t lo = 0x0f0f0f0fu;
-                const uint2 c0 = make_uint2(mxfp4_kv4((q0[bl].x >> nsh) & lo), mxfp4_kv4((q0[bl].y >> nsh) & lo));
-                const v4i d0 = mfma16x16x32(a[bl], c0);
-                const float sc0 = mxfp4_scale_half(e0[bl]);
+                const uint2 a = *((const uint2 *)&aq_l[wave][i][0] + 4u * bl + a_piece);
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    if (d0[r] != 0) f0[r] += sc0 * (float)d0[r];
-                if (PAIR) {
-                    const uint2 c1 =
-                        make_uint2(mxfp4_kv4((q1[bl].x >> nsh) & lo), mxfp4_kv4((q1[bl].y >> nsh) & lo));
-                    const v4i d1 = mfma16x16x32(a[bl], c1);
-                    const float sc1 = mxfp4_scale_half(e1[bl]);
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    const uint2 qq = *((const uint2 *)&wq_l[wave][mt][i][bl] + (kq >> 1));
+                    const uint32_t lo = 0x0f0f0f0fu;
+                    const uint2 c = make_uint2(mxfp4_kv4((qq.x >> nsh) & lo), mxfp4_kv4((qq.y >> nsh) & lo));
+                    const v4i d = mfma16x16x32(a, c);
+                    const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
+                    // = the reference's `if (sumi != 0) sumf += sc * sumi`: sc
+                    // is 0 or a power of two and |sumi| < 2^24, so sc * sumi is
+                    // exact and one fma rounds like the multiply-add; a zero
+                    // sumi adds +0, which leaves sumf (never -0) unchanged
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (d1[r] != 0) f1[r] += sc1 * (float)d1[r];
+                    for (int r = 0; r < 4; r++) f[mt][r] = __builtin_fmaf(sc, (float)d[r], f[mt][r]);
                 }
             }
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                sbval[sb * sv_stride + i * 17u + 4u * kq + r] = yd[r] * f0[r];
-                if (PAIR) sbval[(k_blocks + sb) * sv_stride + i * 17u + 4u * kq + r] = yd[r] * f1[r];
-            }
+            for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[mt][r] += yd[r] * f[mt][r];
         }
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) part[wave][mt][i][4u * kq + r] = acc[mt][r];
         __syncthreads();
-        // one thread per (row, pair): the super-blocks in order, then the epilogue
+        // one thread per (row, pair): the 4 ranges in order, then the epilogue
         const uint32_t ri = threadIdx.x & 15u, pi = threadIdx.x >> 4;
         if (pi < m && row0 + ri < n_rows) {
-            float g = 0.0f, u = 0.0f;
-            for (uint32_t sb = 0; sb < k_blocks; sb++) {
-                g += sbval[sb * sv_stride + ri * 17u + pi];
-                if (PAIR) u += sbval[(k_blocks + sb) * sv_stride + ri * 17u + pi];
-            }
+            const float g = ((part[0][0][ri][pi] + part[1][0][ri][pi]) + part[2][0][ri][pi]) + part[3][0][ri][pi];
             const uint32_t pr = pr_l[pi];
             const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
             const uint32_t orow = row0 + ri;
             if (PAIR) {
-                if (p.gate_b) g += ldwf(p.gate_b + orow);
+                float u = ((part[0][NM - 1][ri][pi] + part[1][NM - 1][ri][pi]) + part[2][NM - 1][ri][pi]) +
+                          part[3][NM - 1][ri][pi];
+                float gg = g;
+                if (p.gate_b) gg += ldwf(p.gate_b + orow);
                 if (p.up_b) u += ldwf(p.up_b + orow);
-                out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
+                out[so * n_rows + orow] = glu(gg, u, act_op) * weights[so];
             } else {
                 out[so * n_rows + orow] = g;
             }
@@ -416,9 +426,8 @@ int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const voi
                              const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
                              uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
     const uint32_t k_blocks = (k_dim + 255u) / 256u;
-    if (k_blocks > kMmqMaxSb) return reject("moe grouped mxfp4 (row width above 8192)");
     const dim3 grid((n_rows + 15u) / 16u, n_group);
-    const size_t lds = (size_t)(pair ? 2u : 1u) * k_blocks * 16u * 17u * sizeof(float);
+    const size_t lds = 0;
     if (pair)
         hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<true>, grid, dim3(256), lds, pk::stream(), out,
                            (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,

@@ -422,9 +422,11 @@ struct Fmt<PULSAR_QUANT_MXFP4> {
     PK_DEV static Part part(const W &w, const Act &a, uint32_t, const uint2 *) {
         const int32_t s0 = mxfp4_block(w.q0, a.q[0], a.q[1]);
         const int32_t s1 = w.two ? mxfp4_block(w.q1, a.q[2], a.q[3]) : 0;  // select, both computed
-        float f = 0.0f;
-        if (s0 != 0) f += mxfp4_scale_half(w.e & 0xffu) * (float)s0;
-        if (s1 != 0) f += mxfp4_scale_half(w.e >> 8) * (float)s1;
+        // fma == the reference's multiply-add here (exact product of a power
+        // of two and an int < 2^24), and a zero sum adds +0, which leaves a
+        // sum that is never -0 unchanged: no test on s0 / s1 needed
+        float f = __builtin_fmaf(mxfp4_scale_half(w.e & 0xffu), (float)s0, 0.0f);
+        f = __builtin_fmaf(mxfp4_scale_half(w.e >> 8), (float)s1, f);
         return Part{s0, s1, f};
     }
     // y->d * sumf
