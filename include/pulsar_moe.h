@@ -202,6 +202,14 @@ int pulsar_moe_route_ptrs(void *ptrs, void *slot_weights, const void *selected,
 int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, const void *ptrs,
                          uint32_t n_tok, uint32_t n_used, uint32_t max_groups);
 
+/* Self-checks: small device runs of the entry points compared with host
+ * mirrors (q8_K bit-exact; every stage of the MoE path for Q2_K, IQ2_XXS,
+ * Q4_K, Q6_K and MXFP4; router modes 0, 1 and 2). They allocate and
+ * synchronise, print one line per case to stderr and return 1 when all pass.
+ * Replace pulsar_kernels.cu:6421-6460 and 1271-1285. */
+int pulsar_moe_selftest(void);
+int pulsar_router_selftest(void);
+
 /* ---- fused decode layer (no reference counterpart: the reference runs
  * these steps as separate launches with a host round trip in between,
  * crates/engine/src/lib.rs:7663-7670, 8416-8510). Each call produces

@@ -18,7 +18,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libpulsar_moe.so"
-SOURCES = ["q8k.hip", "matvec.hip", "mmq.hip", "moe.hip", "router.hip", "route.hip", "fused.hip"]
+SOURCES = ["q8k.hip", "matvec.hip", "mmq.hip", "moe.hip", "router.hip", "route.hip", "fused.hip", "selftest.hip"]
 ARCH = os.environ.get("PULSAR_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: fp32 epilogues must round in source order (the reference

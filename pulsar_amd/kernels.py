@@ -197,6 +197,16 @@ def moe_down_f32(out, ptrs, slot_weights, mid, mid_dim: int, out_dim: int, n_use
                                            n_used, n_tok, row_bytes, quant, int(bool(add_bias))), "moe_down_f32")
 
 
+def moe_selftest() -> bool:
+    """pulsar_moe_selftest (klib:1563): the MoE path per format against host mirrors."""
+    return bool(_lib.load().pulsar_moe_selftest())
+
+
+def router_selftest() -> bool:
+    """pulsar_router_selftest (klib:1559)."""
+    return bool(_lib.load().pulsar_router_selftest())
+
+
 def set_stream(stream) -> None:
     """Routes later launches from this thread to `stream` (a torch Stream, a
     raw hipStream_t int, or None for the null stream)."""

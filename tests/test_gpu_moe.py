@@ -364,3 +364,10 @@ def test_graph_replays_match_eager(dev):
         assert np.array_equal(down(out), eager)
         chain()  # eager work between replays
         assert np.array_equal(down(out), eager)
+
+
+def test_library_selftests(dev):
+    """pulsar_moe_selftest / pulsar_router_selftest: the library's own checks
+    against its host mirrors (the reference ABI's self-test entry points)."""
+    assert K.router_selftest()
+    assert K.moe_selftest()
