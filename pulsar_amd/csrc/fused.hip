@@ -23,7 +23,7 @@ constexpr uint32_t kFusedMaxSlots = 64;    // k_used + n_shared
 constexpr uint32_t kFusedMaxActLds = 65536; // staged mid rows of one token
 
 #define PK_FUSED_IQ2_LUT(Q)                                         \
-    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? 256 : 1];    \
+    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];    \
     if ((Q) == PULSAR_QUANT_IQ2_XXS) {                              \
         fill_iq2xxs_lut(lut);                                       \
         __syncthreads();                                            \

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
                                                      uint32_t lpr_log2, uint32_t in_blocks,
                                                      uint32_t out_dim, uint32_t n_tok,
                                                      uint64_t row_bytes, uint32_t n_pass) {
-    __shared__ uint2 lut[Q == PULSAR_QUANT_IQ2_XXS ? 256 : 1];
+    __shared__ uint2 lut[Q == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];
     if (Q == PULSAR_QUANT_IQ2_XXS) {
         fill_iq2xxs_lut(lut);
         __syncthreads();
@@ -77,78 +77,12 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
     }
 }
 
-// LDS-tiled variant: the block stages `tile_rows` consecutive rows (one
-// contiguous byte span of the matrix) with dense 16-byte loads - every
-// wave-wide load instruction reads 1 KiB of whole cache lines - then each
-// wave decodes its row passes from LDS with the same unit decoders.
-constexpr uint32_t kTileMax = 32768;  // bytes of one staged tile
-
-template <uint32_t Q, uint32_t T, uint32_t UPLMAX>
-__global__ __launch_bounds__(256) void matvec_lds_kernel(float *__restrict__ out,
-                                                         const uint8_t *__restrict__ w,
-                                                         const pulsar_block_q8_K *__restrict__ xq,
-                                                         uint32_t n_units, uint32_t nblk32,
-                                                         uint32_t lpr_log2, uint32_t in_blocks,
-                                                         uint32_t out_dim, uint32_t n_tok,
-                                                         uint64_t row_bytes, uint32_t tile_rows) {
-    __shared__ uint2 lut[Q == PULSAR_QUANT_IQ2_XXS ? 256 : 1];
-    __shared__ uint4 tile[kTileMax / 16 + 1];
-    if (Q == PULSAR_QUANT_IQ2_XXS) fill_iq2xxs_lut(lut);
-    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
-    const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t t0 = blockIdx.y * T;
-    Act a[T][UPLMAX];
-#pragma unroll
-    for (uint32_t t = 0; t < T; t++) {
-        const uint32_t tok = t0 + t < n_tok ? t0 + t : n_tok - 1u;
-        load_row_acts<Q, UPLMAX>(xq + (uint64_t)tok * in_blocks, rg, a[t]);
-    }
-    const uint32_t wave = threadIdx.x / 64u;
-    const uint32_t n_tiles = (out_dim + tile_rows - 1u) / tile_rows;
-    const uint32_t passes = tile_rows / rpp;  // a multiple of the 4 waves
-    for (uint32_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x) {
-        const uint32_t r0 = ti * tile_rows;
-        const uint32_t nr = out_dim - r0 < tile_rows ? out_dim - r0 : tile_rows;
-        const uint64_t start = (uint64_t)r0 * row_bytes;
-        const uint64_t end = start + (uint64_t)nr * row_bytes;
-        // 16-byte granules covering [start, end): the first may begin up to
-        // 15 bytes early and the last end up to 15 bytes late, both inside
-        // the granules (hence the pages) the rows themselves occupy
-        const uintptr_t g0 = ((uintptr_t)(w + start)) & ~(uintptr_t)15;
-        const uint32_t shift = (uint32_t)((uintptr_t)(w + start) - g0);
-        const uint32_t n16 = (uint32_t)((shift + (end - start) + 15u) / 16u);
-        __syncthreads();  // the previous tile's readers are done
-        for (uint32_t c = threadIdx.x; c < n16; c += blockDim.x) tile[c] = *(const uint4 *)(g0 + 16u * c);
-        __syncthreads();
-        const uint8_t *tb = (const uint8_t *)tile + shift;
-        for (uint32_t p = wave; p < passes; p += 4u) {
-            const uint32_t rl = p * rpp + rg.rip;
-            const bool row_ok = rl < nr;
-            typename Fmt<Q>::W wu[UPLMAX];
-            load_row_w<Q, UPLMAX>(tb + (uint64_t)(row_ok ? rl : 0u) * row_bytes, rg, wu);
-#pragma unroll
-            for (uint32_t t = 0; t < T; t++) {
-                float acc = row_partial<Q, UPLMAX>(row_ok, rg, wu, a[t], lut);
-                acc = row_finish(acc, rg);
-                if (row_ok && rg.holds_row() && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + r0 + rl] = acc;
-            }
-        }
-    }
-}
-
 #ifndef PK_MV_RPW
 #define PK_MV_RPW 1
 #endif
 #ifndef PK_MV_WAVES
 #define PK_MV_WAVES 4096u
 #endif
-#ifndef PK_MV_TILE
-#define PK_MV_TILE 16384u
-#endif
-#ifndef PK_MV_BLOCKS
-#define PK_MV_BLOCKS 2048u
-#endif
-
 template <uint32_t Q, uint32_t T, uint32_t UPLMAX, uint32_t RPW>
 static void launch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t n_units,
                           uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t out_dim,
@@ -177,23 +111,6 @@ static int dispatch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K
     const uint32_t upl = (n_units + (1u << l2) - 1u) >> l2;
     const uint32_t in_blocks = (in_dim + 255u) / 256u;
     const uint32_t nblk32 = (in_dim + 31u) / 32u;
-#ifdef PK_MV_LDS
-    {
-        const uint32_t rpp = 64u >> l2;
-        uint32_t tile_rows = (uint32_t)(PK_MV_TILE / row_bytes) / (4u * rpp) * (4u * rpp);
-        if (tile_rows >= 4u * rpp && upl <= 1u && n_tok <= 2u) {
-            const uint32_t n_tiles = (out_dim + tile_rows - 1u) / tile_rows;
-            const uint32_t grid = n_tiles < PK_MV_BLOCKS ? n_tiles : PK_MV_BLOCKS;
-            if (n_tok == 1u)
-                hipLaunchKernelGGL((matvec_lds_kernel<Q, 1, 1>), dim3(grid, 1), dim3(256), 0, pk::stream(), out, w,
-                                   xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes, tile_rows);
-            else
-                hipLaunchKernelGGL((matvec_lds_kernel<Q, 2, 1>), dim3(grid, 1), dim3(256), 0, pk::stream(), out, w,
-                                   xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes, tile_rows);
-            return launch_ok("matmul_kq launch");
-        }
-    }
-#endif
 #define PK_MV(T, U, R) launch_matvec<Q, T, U, R>(out, w, xq, n_units, nblk32, l2, in_blocks, out_dim, n_tok, row_bytes)
     if (upl <= 1u) {
         if (n_tok == 1u)

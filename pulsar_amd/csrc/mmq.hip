@@ -377,8 +377,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
                     const uint2 qq = *((const uint2 *)&wq_l[wave][mt][i][bl] + (kq >> 1));
-                    const uint32_t lo = 0x0f0f0f0fu;
-                    const uint2 c = make_uint2(mxfp4_kv4((qq.x >> nsh) & lo), mxfp4_kv4((qq.y >> nsh) & lo));
+                    const uint2 c = make_uint2(mxfp4_kv4(qq.x >> nsh), mxfp4_kv4(qq.y >> nsh));
                     const v4i d = mfma16x16x32(a, c);
                     const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
                     // = the reference's `if (sumi != 0) sumf += sc * sumi`: sc

@@ -19,7 +19,7 @@ constexpr uint32_t kWaves = 4;      // waves per block
 constexpr uint32_t kSlotChunk = 32; // down-stage slots staged in LDS per round
 
 #define PK_IQ2_LUT(Q)                                               \
-    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? 256 : 1];    \
+    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];    \
     if ((Q) == PULSAR_QUANT_IQ2_XXS) {                              \
         fill_iq2xxs_lut(lut);                                       \
         __syncthreads();                                            \

@@ -170,8 +170,9 @@ struct Fmt<PULSAR_QUANT_Q4_K> {
         scale_min(w.hdr, 2 * u, sc1, m1);
         scale_min(w.hdr, 2 * u + 1, sc2, m2);
         Part p;
-        p.i0 = sc1 * s1 + sc2 * s2;
-        p.i1 = m1 * (a.bs[0] + a.bs[1]) + m2 * (a.bs[2] + a.bs[3]);
+        // every factor fits 24 bits signed: full-rate v_mul_i32_i24
+        p.i0 = __mul24(sc1, s1) + __mul24(sc2, s2);
+        p.i1 = __mul24(m1, a.bs[0] + a.bs[1]) + __mul24(m2, a.bs[2] + a.bs[3]);
         p.f = 0.0f;
         return p;
     }
@@ -237,7 +238,7 @@ struct Fmt<PULSAR_QUANT_Q6_K> {
         int32_t isum = 0;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            isum += sc[q] * (dot16(c[q][0], c[q][1], c[q][2], c[q][3], a.q[q], 0) - 32 * a.bs[q]);
+            isum += __mul24(sc[q], dot16(c[q][0], c[q][1], c[q][2], c[q][3], a.q[q], 0) - 32 * a.bs[q]);
         return Part{isum, 0, 0.0f};
     }
     // d * y->d * isum with d = x->d (pulsar_kernels.cu:5946)
@@ -282,8 +283,8 @@ struct Fmt<PULSAR_QUANT_Q2_K> {
             const int32_t d = dot16((w.qs.x >> sh) & m2, (w.qs.y >> sh) & m2, (w.qs.z >> sh) & m2,
                                     (w.qs.w >> sh) & m2, a.q[s], 0);
             const uint32_t scb = byte_of(w.sc, 2u * s + half);
-            isum += (int32_t)(scb & 0x0fu) * d;
-            summs += a.bs[s] * (int32_t)(scb >> 4);
+            isum += __mul24((int32_t)(scb & 0x0fu), d);
+            summs += __mul24(a.bs[s], (int32_t)(scb >> 4));
         }
         return Part{isum, summs, 0.0f};
     }
@@ -299,17 +300,17 @@ struct Fmt<PULSAR_QUANT_Q2_K> {
 // block_iq2_xxs (pulsar_kernels.cu:1303-1306): f16 d @0, then per 32-group
 // aux0 (4 grid indices) and aux1 (4 x 7 sign bits, 4-bit scale in 28..31).
 // Dot: cpu_dot.rs:92-122. The grid lives in LDS as 256 x 8 magnitude bytes.
+// The LDS table holds the 256 grid rows (8 magnitude bytes each) and, at
+// kIq2SignRow + s7, the 8-byte mask of the 7-bit sign field s7: 0xff in
+// byte j when value j is negated.
+constexpr uint32_t kIq2SignRow = 256u, kIq2LutRows = 256u + 128u;
 PK_DEV void iq2_signed8(const uint2 *lut, uint32_t idx, uint32_t s7, uint32_t &w0, uint32_t &w1) {
     const uint2 g = lut[idx];
-    // sign_mask (cpu_dot.rs:66-70): bit 7 completes even parity
-    const uint32_t s = s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
-    // spread sign bits 0..3 / 4..7 to the low bit of each byte
-    const uint32_t m0 = ((s & 0x0fu) * 0x00204081u) & 0x01010101u;
-    const uint32_t m1 = (((s >> 4) & 0x0fu) * 0x00204081u) & 0x01010101u;
-    // per-byte two's-complement negation where the bit is set; magnitudes
+    const uint2 m = lut[kIq2SignRow + s7];
+    // per-byte two's-complement negation where the mask is set; magnitudes
     // are 8, 25 or 43, so (~g + 1) never carries into the next byte
-    w0 = (g.x ^ (m0 * 0xffu)) + m0;
-    w1 = (g.y ^ (m1 * 0xffu)) + m1;
+    w0 = (g.x ^ m.x) + (m.x & 0x01010101u);
+    w1 = (g.y ^ m.y) + (m.y & 0x01010101u);
 }
 
 template <>
@@ -336,7 +337,7 @@ struct Fmt<PULSAR_QUANT_IQ2_XXS> {
             iq2_signed8(lut, (aux0 >> (8 * k)) & 0xffu, (aux1 >> (7 * k)) & 127u, w[2 * k], w[2 * k + 1]);
         int32_t sumi = dot16(w[0], w[1], w[2], w[3], a0, 0);
         sumi = dot16(w[4], w[5], w[6], w[7], a1, sumi);
-        return sumi * (int32_t)(2u * (aux1 >> 28) + 1u);
+        return __mul24(sumi, (int32_t)(2u * (aux1 >> 28) + 1u));
     }
     PK_DEV static Part part(const W &w, const Act &a, uint32_t, const uint2 *lut) {
         const int32_t b0 = group(lut, w.aux.x, w.aux.y, a.q[0], a.q[1]);
@@ -351,7 +352,8 @@ struct Fmt<PULSAR_QUANT_IQ2_XXS> {
 };
 
 // Fills an LDS copy of the IQ2_XXS grid (256 x 8 bytes) from the base-3
-// codes; call from all threads of the block, then __syncthreads().
+// codes and the 128 sign masks after it (kIq2LutRows rows in all); call
+// from all threads of the block, then __syncthreads().
 __device__ static const uint16_t k_iq2xxs_codes[256] = {PULSAR_IQ2XXS_GRID_CODES};
 PK_DEV void fill_iq2xxs_lut(uint2 *lut) {
     for (uint32_t i = threadIdx.x; i < 256u; i += blockDim.x) {
@@ -366,6 +368,15 @@ PK_DEV void fill_iq2xxs_lut(uint2 *lut) {
         lut[i] = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
                             b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
     }
+    for (uint32_t s7 = threadIdx.x; s7 < 128u; s7 += blockDim.x) {
+        // sign_mask (cpu_dot.rs:66-70): bit 7 completes even parity
+        const uint32_t s = s7 | ((uint32_t)(__builtin_popcount(s7) & 1) << 7);
+        uint32_t m[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if ((s >> j) & 1u) m[j >> 2] |= 0xffu << (8 * (j & 3));
+        lut[kIq2SignRow + s7] = make_uint2(m[0], m[1]);
+    }
 }
 
 // --------------------------------------------------------------- MXFP4 ---
@@ -373,24 +384,36 @@ PK_DEV void fill_iq2xxs_lut(uint2 *lut) {
 // nibble = value i, high = i + 16). Rows pack 17-byte blocks. Dot:
 // pulsar_kernels.cu:5715-5741 with the doubled E2M1 table and the
 // 2^(e-128) scale (e < 2 flushes to 0).
-PK_DEV uint32_t mxfp4_kv4(uint32_t nib) {
-    // doubled E2M1 magnitudes {0,1,2,3,4,6,8,12} and their negatives,
-    // selected per byte by v_perm_b32 on the low 3 bits, then blended on bit 3
-    const uint32_t sel = nib & 0x07070707u;
+// Doubled E2M1 values {0,1,2,3,4,6,8,12} and their negatives, selected per
+// byte by v_perm_b32 on the code's low 3 bits and blended on its sign bit.
+// The blend mask comes from v_perm_b32 too: selectors 8, 9, 10, 11 give
+// 0xff / 0x00 from bit 15 / 31 of the low source word and bit 15 / 31 of
+// the high one, so each byte's sign bit is first moved to one of those.
+PK_DEV uint32_t mxfp4_pick(uint32_t sel, uint32_t m) {
     const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);
     const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);
-    const uint32_t m = ((nib >> 3) & 0x01010101u) * 0xffu;
     return (neg & m) | (pos & ~m);
+}
+// codes in bits 0..3 of each byte of n (bits 4..7 ignored)
+PK_DEV uint32_t mxfp4_kv4(uint32_t n) {
+    // byte k's sign (bit 8k + 3) -> bit 15 / 31 of (n << 12) for k = 0, 2
+    // and of (n << 4) for k = 1, 3
+    const uint32_t m = __builtin_amdgcn_perm(n << 12, n << 4, 0x090B080Au);
+    return mxfp4_pick(n & 0x07070707u, m);
+}
+// codes in bits 4..7 of each byte of q
+PK_DEV uint32_t mxfp4_kv4_hi(uint32_t q) {
+    // byte k's sign (bit 8k + 7) -> bit 15 / 31 of (q << 8) for k = 0, 2
+    // and of q for k = 1, 3
+    const uint32_t m = __builtin_amdgcn_perm(q << 8, q, 0x090B080Au);
+    return mxfp4_pick((q >> 4) & 0x07070707u, m);
 }
 PK_DEV float mxfp4_scale_half(uint32_t e) {
     return e < 2u ? 0.0f : __builtin_bit_cast(float, (e - 1u) << 23);
 }
 PK_DEV int32_t mxfp4_block(uint4 q, uint4 a0, uint4 a1) {
-    const uint32_t lo = 0x0f0f0f0fu;
-    int32_t s = dot16(mxfp4_kv4(q.x & lo), mxfp4_kv4(q.y & lo), mxfp4_kv4(q.z & lo),
-                      mxfp4_kv4(q.w & lo), a0, 0);
-    s = dot16(mxfp4_kv4((q.x >> 4) & lo), mxfp4_kv4((q.y >> 4) & lo), mxfp4_kv4((q.z >> 4) & lo),
-              mxfp4_kv4((q.w >> 4) & lo), a1, s);
+    int32_t s = dot16(mxfp4_kv4(q.x), mxfp4_kv4(q.y), mxfp4_kv4(q.z), mxfp4_kv4(q.w), a0, 0);
+    s = dot16(mxfp4_kv4_hi(q.x), mxfp4_kv4_hi(q.y), mxfp4_kv4_hi(q.z), mxfp4_kv4_hi(q.w), a1, s);
     return s;
 }
 
