@@ -21,10 +21,13 @@ namespace pk {
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 
+PK_DEV v4i mfma16x16x32(uint2 a, uint2 b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), c, 0,
+                                                 0, 0);
+}
 PK_DEV v4i mfma16x16x32(uint2 a, uint2 b) {
     const v4i z = {0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a), __builtin_bit_cast(long, b), z, 0,
-                                                 0, 0);
+    return mfma16x16x32(a, b, z);
 }
 
 // LDS loads at aligned offsets
@@ -435,6 +438,303 @@ int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const voi
         hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<false>, grid, dim3(256), lds, pk::stream(), out,
                            (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
                            weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op);
+    return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
+}
+
+// ----------------------------------------- grouped Q2_K / IQ2_XXS (MoE) --
+// Block = 64 rows (16 per wave) x up to kGqPairs pairs of one expert group,
+// the whole K per wave (no split). The pairs' q8_K rows are staged in LDS
+// once per pair tile (load_act_lds layout); each wave streams its 16 rows
+// super-block by super-block: a contiguous copy (consecutive lanes on
+// consecutive bytes of a row) to registers, the next super-block's copy in
+// flight while the current one, moved to the wave's LDS slot, is decoded.
+// Lane group kq holds values 32t + 8kq + [0, 8) of K slice t (32 values);
+// A = the pairs' q8 values (lanes of pairs past the tile read zeros),
+// B = the rows' signed int8 weights; D lane (row i, kq) holds pairs 4kq + r.
+//
+// Q2_K (84 B: scales[16] @0, qs[64] @16, f16 d, dmin @80): value
+// 32t + 8kq + i sits in qs byte 32(t / 4) + 16(kq / 2) + 8(kq % 2) + i at
+// bits 2(t % 4), sub-block 2t + kq / 2. Codes are pre-scaled by their
+// sub-block scale (3 x 15 fits int8: v_perm_b32 picks from the bytes
+// {0, sc, 2sc, 3sc}), so the 8 chained MFMAs of a super-block give
+// isum = sum_c (sc_c & 15) sum q q8 exactly; summs = sum_c bsums_c
+// (sc_c >> 4) comes from two MFMAs on bsums split as 128 h + l, l in
+// [0, 128). Super-block value yd xd isum - yd xmin summs (cpu_dot.rs:732-767).
+// IQ2_XXS (66 B: f16 d @0, 8 x {aux0, aux1} @2): lane group kq holds grid
+// entry kq of each 32-group (8 values, signed through the LDS sign table);
+// one MFMA per group gives sumi, bsum += sumi (2 (aux1 >> 28) + 1), super-
+// block value 0.125 xd yd bsum (cpu_dot.rs:92-122).
+// Per (row, pair) the super-block values are added in order; the row's
+// value is then complete (no cross-wave sum).
+template <uint32_t Q>
+struct GmmqFmt;
+template <>
+struct GmmqFmt<PULSAR_QUANT_Q2_K> {
+    static constexpr uint32_t kSb = 84;
+    static constexpr uint32_t kPieces = 5;     // 16-byte copies: bytes 0..79 to slot 0..79
+    static constexpr uint32_t kSrc0 = 0;       // first copied byte
+    static constexpr uint32_t kTailSrc = 80;   // d, dmin (4 bytes) ...
+    static constexpr uint32_t kTailSlot = 80;  // ... to slot 80
+};
+template <>
+struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
+    static constexpr uint32_t kSb = 66;
+    static constexpr uint32_t kPieces = 4;     // bytes 2..65 (the groups) to slot 0..63
+    static constexpr uint32_t kSrc0 = 2;
+    static constexpr uint32_t kTailSrc = 0;    // d (read as 4 bytes, the upper 2 unused) ...
+    static constexpr uint32_t kTailSlot = 64;  // ... to slot 64
+};
+#ifndef PK_GQ_PITCH
+#define PK_GQ_PITCH 144u
+#endif
+#ifndef PK_GQ_ACT_LDS
+#define PK_GQ_ACT_LDS 24576u
+#endif
+constexpr uint32_t kGqRowPitch = PK_GQ_PITCH;  // LDS bytes per row slot (36 dwords: 16 rows in distinct banks)
+constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
+constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
+
+// Two packed int16 -> two bytes (low bytes), for the bsums split
+typedef short pk_short2 __attribute__((ext_vector_type(2)));
+PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
+    if (high) {  // h = b >> 7 (arithmetic), |h| <= 16
+        x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, x) >> (short)7);
+        y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, y) >> (short)7);
+    } else {  // l = b & 127
+        x &= 0x007f007fu;
+        y &= 0x007f007fu;
+    }
+    return __builtin_amdgcn_perm(y, x, 0x06040200u);  // bytes 0, 2 of x, then of y
+}
+
+template <uint32_t Q, bool PAIR>
+__global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
+        float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
+        const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
+        const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t n_rows, uint32_t n_used,
+        uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
+    using F = GmmqFmt<Q>;
+    constexpr uint32_t NM = PAIR ? 2 : 1;
+    constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
+    constexpr uint32_t kWp = NM * 16u * F::kPieces;  // weight pieces per super-block
+    constexpr uint32_t kWj = (kWp + 63u) / 64u;     // ... per lane
+    extern __shared__ __align__(16) uint8_t acts_lds[];
+    __shared__ uint2 lut[kIq2 ? kIq2LutRows : 1];
+    __shared__ __align__(16) uint8_t wl[4][NM][16][kGqRowPitch];  // [wave][matrix][row] super-block slot
+    __shared__ uint32_t pr_l[kGqPairs];
+    if (kIq2) {
+        fill_iq2xxs_lut(lut);
+        __syncthreads();
+    }
+    const uint32_t group = blockIdx.y;
+    const pulsar_expert_ptrs p = gptrs[group];
+    const uint8_t *w0 = PAIR ? (const uint8_t *)p.gate : (const uint8_t *)p.down;
+    const uint8_t *w1 = PAIR ? (const uint8_t *)p.up : nullptr;
+    if (!w0 || (PAIR && !w1)) return;
+    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    if (s0 >= s1) return;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t i = lane & 15u, kq = lane >> 4;
+    const uint32_t rw0 = blockIdx.x * 64u + wave * 16u;  // the wave's first row
+    const bool active = rw0 < n_rows;                    // wave-uniform
+    // weight copy: piece q = lane + 64 j is piece q % kPieces of row
+    // (q / kPieces) % 16 of matrix q / (16 kPieces)
+    const uint8_t *wsrc[kWj];
+    uint32_t wdst[kWj];
+#pragma unroll
+    for (uint32_t j = 0; j < kWj; j++) {
+        const uint32_t q = lane + 64u * j;
+        const uint32_t mt = q / (16u * F::kPieces), rem = q % (16u * F::kPieces);
+        const uint32_t r = rem / F::kPieces, c = rem % F::kPieces;
+        const uint32_t gr = rw0 + r < n_rows ? rw0 + r : n_rows - 1u;
+        wsrc[j] = as_global(PAIR && mt ? w1 : w0) + (uint64_t)gr * row_bytes + F::kSrc0 + 16u * c;
+        wdst[j] = q < kWp ? ((mt * 16u + r) * kGqRowPitch + 16u * c) : UINT32_MAX;
+    }
+    // tails (d / dmin): lanes 0 .. 16 NM - 1, row lane % 16 of matrix lane / 16
+    const uint32_t tr = rw0 + (lane & 15u) < n_rows ? rw0 + (lane & 15u) : n_rows - 1u;
+    const uint8_t *tsrc = as_global(PAIR && lane >= 16u ? w1 : w0) + (uint64_t)tr * row_bytes + F::kTailSrc;
+    const bool t_on = lane < 16u * NM;
+    const uint32_t tdst = ((lane >> 4) * 16u + (lane & 15u)) * kGqRowPitch + F::kTailSlot;
+    uint8_t *wl_w = &wl[wave][0][0][0];
+    const uint32_t act_bytes = k_blocks * kActLdsPitch;
+    for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
+        const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
+        if (t0 != s0) __syncthreads();  // the previous tile's activations are consumed
+        if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
+        __syncthreads();
+        stage_q8_rows<2>(acts_lds, m, k_blocks, [&](uint32_t j) {
+            const uint32_t pr = pr_l[j];
+            return act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) * k_blocks;
+        });
+        __syncthreads();
+        if (!active) continue;  // wave-uniform; the block's barriers above are reached
+        uint4 wv[kWj];
+        uint32_t tv = 0u;
+        auto issue = [&](uint32_t sb) {
+            const uint64_t wo = (uint64_t)sb * F::kSb;
+#pragma unroll
+            for (uint32_t j = 0; j < kWj; j++)
+                if (wdst[j] != UINT32_MAX) wv[j] = ldw128(wsrc[j] + wo);
+            if (t_on) tv = ldw32(tsrc + wo);
+        };
+        // lane (pair i, kq): its pair's record, or none past the tile
+        const bool a_on = i < m;
+        const uint8_t *ar = acts_lds + (a_on ? i : 0u) * act_bytes;
+        float acc[NM][4];
+#pragma unroll
+        for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
+        issue(0);
+        for (uint32_t sb = 0; sb < k_blocks; sb++) {
+#pragma unroll
+            for (uint32_t j = 0; j < kWj; j++)
+                if (wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
+            if (t_on) *(uint32_t *)(wl_w + tdst) = tv;
+            // the wave's own LDS slot: visible to the wave's other lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (sb + 1u < k_blocks) issue(sb + 1u);  // in flight while this one is decoded
+            const uint8_t *rec = ar + sb * kActLdsPitch;  // d @0, q8 values @16, bsums @272
+            float yd[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t pi = 4u * kq + r;
+                yd[r] = pi < m ? *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch) : 0.0f;
+            }
+            auto a_at = [&](uint32_t t) {
+                return a_on ? *(const uint2 *)(rec + 16u + 32u * t + 8u * kq) : make_uint2(0u, 0u);
+            };
+            if constexpr (!kIq2) {
+                uint4 sc[NM];
+                uint2 qv[NM][2];
+                v4i isum[NM];
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    const uint8_t *ws = wl_w + (mt * 16u + i) * kGqRowPitch;
+                    sc[mt] = *(const uint4 *)ws;
+#pragma unroll
+                    for (uint32_t k = 0; k < 2; k++)
+                        qv[mt][k] = *(const uint2 *)(ws + 16u + 32u * k + 16u * (kq >> 1) + 8u * (kq & 1u));
+                    isum[mt] = v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (uint32_t t = 0; t < 8; t++) {
+                    const uint2 a = a_at(t);
+                    const uint32_t sbi = 2u * t + (kq >> 1);  // sub-block
+                    const uint32_t sh = 2u * (t & 3u);
+#pragma unroll
+                    for (uint32_t mt = 0; mt < NM; mt++) {
+                        const uint32_t scw[4] = {sc[mt].x, sc[mt].y, sc[mt].z, sc[mt].w};
+                        const uint32_t scv = (scw[sbi >> 2] >> (8u * (sbi & 3u))) & 0x0fu;
+                        const uint32_t tab = __umul24(scv, 0x030201u) << 8;  // {0, sc, 2sc, 3sc}
+                        const uint2 q = qv[mt][t >> 2];
+                        const uint2 b = make_uint2(__builtin_amdgcn_perm(0u, tab, (q.x >> sh) & 0x03030303u),
+                                                   __builtin_amdgcn_perm(0u, tab, (q.y >> sh) & 0x03030303u));
+                        isum[mt] = mfma16x16x32(a, b, isum[mt]);
+                    }
+                }
+                // lane (pair i, kq): l (kq < 2) or h (kq >= 2) bytes of bsums 8 (kq & 1) + [0, 8)
+                uint2 alh = make_uint2(0u, 0u);
+                if (a_on) {
+                    const uint4 bs = *(const uint4 *)(rec + 272u + 16u * (kq & 1u));
+                    alh = make_uint2(bsum_bytes(bs.x, bs.y, kq >= 2u), bsum_bytes(bs.z, bs.w, kq >= 2u));
+                }
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    // mins of sub-blocks 8 (kq & 1) + [0, 8) against l (kq < 2) and h (kq >= 2)
+                    const uint2 s8 = (kq & 1u) ? make_uint2(sc[mt].z, sc[mt].w) : make_uint2(sc[mt].x, sc[mt].y);
+                    const uint2 mn = make_uint2((s8.x >> 4) & 0x0f0f0f0fu, (s8.y >> 4) & 0x0f0f0f0fu);
+                    const uint2 zero = make_uint2(0u, 0u);
+                    const v4i dl = mfma16x16x32(alh, kq < 2u ? mn : zero);
+                    const v4i dh = mfma16x16x32(alh, kq < 2u ? zero : mn);
+                    const uint32_t dd = *(const uint32_t *)(wl_w + (mt * 16u + i) * kGqRowPitch + F::kTailSlot);
+                    const float xd = f16f((uint16_t)dd), xmin = f16f((uint16_t)(dd >> 16));
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int32_t summs = dl[r] + 128 * dh[r];
+                        acc[mt][r] += yd[r] * xd * (float)isum[mt][r] - yd[r] * xmin * (float)summs;
+                    }
+                }
+            } else {
+                int32_t bsum[NM][4];
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) bsum[mt][r] = 0;
+#pragma unroll
+                for (uint32_t g = 0; g < 8; g++) {
+                    const uint2 a = a_at(g);
+#pragma unroll
+                    for (uint32_t mt = 0; mt < NM; mt++) {
+                        const uint2 aux = *(const uint2 *)(wl_w + (mt * 16u + i) * kGqRowPitch + 8u * g);
+                        uint2 b;
+                        iq2_signed8(lut, (aux.x >> (8u * kq)) & 0xffu, (aux.y >> (7u * kq)) & 127u, b.x, b.y);
+                        const v4i d = mfma16x16x32(a, b);
+                        const int32_t ls = (int32_t)(2u * (aux.y >> 28) + 1u);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) bsum[mt][r] += __mul24(d[r], ls);
+                    }
+                }
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    const float xd = f16f(*(const uint16_t *)(wl_w + (mt * 16u + i) * kGqRowPitch + F::kTailSlot));
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[mt][r] += 0.125f * xd * yd[r] * (float)bsum[mt][r];
+                }
+            }
+            // this super-block's LDS reads are consumed before the next copy
+            __builtin_amdgcn_wave_barrier();
+        }
+        // lane (row i, kq): pairs 4kq + r of the tile
+        const uint32_t orow = rw0 + i;
+        if (orow < n_rows) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t pi = 4u * kq + r;
+                if (pi >= m) break;
+                const uint32_t pr = pr_l[pi];
+                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+                if (PAIR) {
+                    float g = acc[0][r], u = acc[NM - 1][r];
+                    if (p.gate_b) g += ldwf(p.gate_b + orow);
+                    if (p.up_b) u += ldwf(p.up_b + orow);
+                    out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
+                } else {
+                    out[so * n_rows + orow] = acc[0][r];
+                }
+            }
+        }
+    }
+}
+
+// Grouped MoE stages of Q2_K / IQ2_XXS experts on the matrix cores; -1 for
+// other formats (the caller then uses the lane kernels).
+int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
+                          const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
+                          uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
+    if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS) return -1;
+    const uint32_t k_blocks = k_dim / 256u;
+    const uint32_t per_pair = k_blocks * kActLdsPitch;
+    if (per_pair > kGqActLds) return -1;  // one pair's row does not fit: lane kernels
+    uint32_t pmax = kGqActLds / per_pair;
+    pmax = pmax < kGqPairs ? pmax : kGqPairs;
+    const size_t lds = (size_t)pmax * per_pair;
+    const dim3 grid((n_rows + 63u) / 64u, n_group);
+#define PK_GQ(Q, P)                                                                                              \
+    hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P>), grid, dim3(256), lds, pk::stream(), out,             \
+                       (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs, weights, \
+                       act, k_blocks, n_rows, n_used, row_bytes, act_op, pmax)
+    if (quant == PULSAR_QUANT_Q2_K && pair)
+        PK_GQ(PULSAR_QUANT_Q2_K, true);
+    else if (quant == PULSAR_QUANT_Q2_K)
+        PK_GQ(PULSAR_QUANT_Q2_K, false);
+    else if (pair)
+        PK_GQ(PULSAR_QUANT_IQ2_XXS, true);
+    else
+        PK_GQ(PULSAR_QUANT_IQ2_XXS, false);
+#undef PK_GQ
     return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
 }
 

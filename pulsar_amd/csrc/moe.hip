@@ -464,6 +464,10 @@ namespace pk {
 int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const void *starts, const void *pairs,
                              const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
                              uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
+// mmq.hip: the same for Q2_K / IQ2_XXS experts; -1 for other formats
+int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
+                          const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
+                          uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
 }  // namespace pk
 
 extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *starts,
@@ -486,6 +490,14 @@ extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, cons
         return launch_grouped_mmq_mxfp4(true, (float *)mid, gptrs, starts, pairs, (const float *)weights,
                                         (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group, row_bytes,
                                         act_op);
+#ifndef PK_GRP_LANE_ONLY
+    {
+        const int r = launch_grouped_mmq_kq(true, quant, (float *)mid, gptrs, starts, pairs, (const float *)weights,
+                                            (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group,
+                                            row_bytes, act_op);
+        if (r >= 0) return r;
+    }
+#endif
     const Geo g = geo_for(quant, in_dim);
     PairGroupedLaunch f{mid, gptrs, starts, pairs, weights, xq, mid_dim, n_used, n_group, act_op, row_bytes, g};
     if (!quant_ok(quant)) return reject("moe pair swiglu grouped (quant)");
@@ -506,6 +518,14 @@ extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const v
         return launch_grouped_mmq_mxfp4(false, (float *)partial, gptrs, starts, pairs, nullptr,
                                         (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
                                         row_bytes, 0);
+#ifndef PK_GRP_LANE_ONLY
+    {
+        const int r = launch_grouped_mmq_kq(false, quant, (float *)partial, gptrs, starts, pairs, nullptr,
+                                            (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
+                                            row_bytes, 0);
+        if (r >= 0) return r;
+    }
+#endif
     const Geo g = geo_for(quant, mid_dim);
     DownGroupedLaunch f{partial, gptrs, starts, pairs, midq, out_dim, n_used, n_group, row_bytes, g};
     if (!quant_ok(quant)) return reject("moe down grouped (quant)");
