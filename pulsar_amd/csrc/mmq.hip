@@ -475,6 +475,7 @@ struct GmmqFmt<PULSAR_QUANT_Q2_K> {
     static constexpr uint32_t kSrc0 = 0;       // first copied byte
     static constexpr uint32_t kTailSrc = 80;   // d, dmin (4 bytes) ...
     static constexpr uint32_t kTailSlot = 80;  // ... to slot 80
+    static constexpr uint32_t kSlot = 96;      // LDS bytes per row super-block
 };
 template <>
 struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
@@ -483,16 +484,23 @@ struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
     static constexpr uint32_t kSrc0 = 2;
     static constexpr uint32_t kTailSrc = 0;    // d (read as 4 bytes, the upper 2 unused) ...
     static constexpr uint32_t kTailSlot = 64;  // ... to slot 64
+    static constexpr uint32_t kSlot = 80;
 };
-#ifndef PK_GQ_PITCH
-#define PK_GQ_PITCH 144u
+#ifndef PK_GQ_SBS
+#define PK_GQ_SBS 2u
 #endif
 #ifndef PK_GQ_ACT_LDS
-#define PK_GQ_ACT_LDS 24576u
+#define PK_GQ_ACT_LDS 16384u
 #endif
-constexpr uint32_t kGqRowPitch = PK_GQ_PITCH;  // LDS bytes per row slot (36 dwords: 16 rows in distinct banks)
+constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy step
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
+
+// Per 16-bit half: a * b (low 16 bits), one v_pk_mul_lo_u16
+typedef unsigned short pk_ushort2 __attribute__((ext_vector_type(2)));
+PK_DEV uint32_t pk_mul16(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_ushort2, a) * __builtin_bit_cast(pk_ushort2, b));
+}
 
 // Two packed int16 -> two bytes (low bytes), for the bsums split
 typedef short pk_short2 __attribute__((ext_vector_type(2)));
@@ -516,11 +524,15 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     using F = GmmqFmt<Q>;
     constexpr uint32_t NM = PAIR ? 2 : 1;
     constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
-    constexpr uint32_t kWp = NM * 16u * F::kPieces;  // weight pieces per super-block
-    constexpr uint32_t kWj = (kWp + 63u) / 64u;     // ... per lane
+    constexpr uint32_t S = kGqSbs;
+    constexpr uint32_t kRowL = S * F::kSlot + 16u;        // LDS bytes per row (S slots, padded)
+    constexpr uint32_t kWp = NM * 16u * S * F::kPieces;  // weight pieces per step
+    constexpr uint32_t kWj = (kWp + 63u) / 64u;         // ... per lane
+    constexpr uint32_t kTp = NM * 16u * S;              // tails per step
+    constexpr uint32_t kTj = (kTp + 63u) / 64u;
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint2 lut[kIq2 ? kIq2LutRows : 1];
-    __shared__ __align__(16) uint8_t wl[4][NM][16][kGqRowPitch];  // [wave][matrix][row] super-block slot
+    __shared__ __align__(16) uint8_t wl[4][NM * 16u * kRowL];  // [wave][matrix][row][step slot]
     __shared__ uint32_t pr_l[kGqPairs];
     if (kIq2) {
         fill_iq2xxs_lut(lut);
@@ -537,25 +549,38 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     const uint32_t i = lane & 15u, kq = lane >> 4;
     const uint32_t rw0 = blockIdx.x * 64u + wave * 16u;  // the wave's first row
     const bool active = rw0 < n_rows;                    // wave-uniform
-    // weight copy: piece q = lane + 64 j is piece q % kPieces of row
-    // (q / kPieces) % 16 of matrix q / (16 kPieces)
+    const uint32_t n_steps = (k_blocks + S - 1u) / S;
+    auto row_src = [&](uint32_t mt, uint32_t r) {
+        const uint32_t gr = rw0 + r < n_rows ? rw0 + r : n_rows - 1u;
+        return as_global(PAIR && mt ? w1 : w0) + (uint64_t)gr * row_bytes;
+    };
+    // weight copy: piece q = lane + 64 j is piece q % kPieces of super-block
+    // (q / kPieces) % S of row (q / (kPieces S)) % 16 of matrix q / (16 S
+    // kPieces): consecutive lanes on consecutive bytes of a row's S super-
+    // blocks. Lanes past the last piece load one too (never stored), so
+    // every lane issues the same loads and the waits count them exactly.
     const uint8_t *wsrc[kWj];
-    uint32_t wdst[kWj];
+    uint32_t wsb[kWj], wdst[kWj];
 #pragma unroll
     for (uint32_t j = 0; j < kWj; j++) {
-        const uint32_t q = lane + 64u * j;
-        const uint32_t mt = q / (16u * F::kPieces), rem = q % (16u * F::kPieces);
-        const uint32_t r = rem / F::kPieces, c = rem % F::kPieces;
-        const uint32_t gr = rw0 + r < n_rows ? rw0 + r : n_rows - 1u;
-        wsrc[j] = as_global(PAIR && mt ? w1 : w0) + (uint64_t)gr * row_bytes + F::kSrc0 + 16u * c;
-        wdst[j] = q < kWp ? ((mt * 16u + r) * kGqRowPitch + 16u * c) : UINT32_MAX;
+        const uint32_t q = lane + 64u * j, qq = q < kWp ? q : kWp - 1u;
+        const uint32_t c = qq % F::kPieces, rs = qq / F::kPieces, sl = rs % S, rm = rs / S;
+        wsrc[j] = row_src(rm / 16u, rm % 16u) + F::kSrc0 + 16u * c;
+        wsb[j] = sl;
+        wdst[j] = q < kWp ? (rm * kRowL + sl * F::kSlot + 16u * c) : UINT32_MAX;
     }
-    // tails (d / dmin): lanes 0 .. 16 NM - 1, row lane % 16 of matrix lane / 16
-    const uint32_t tr = rw0 + (lane & 15u) < n_rows ? rw0 + (lane & 15u) : n_rows - 1u;
-    const uint8_t *tsrc = as_global(PAIR && lane >= 16u ? w1 : w0) + (uint64_t)tr * row_bytes + F::kTailSrc;
-    const bool t_on = lane < 16u * NM;
-    const uint32_t tdst = ((lane >> 4) * 16u + (lane & 15u)) * kGqRowPitch + F::kTailSlot;
-    uint8_t *wl_w = &wl[wave][0][0][0];
+    // tails (d / dmin): one per (matrix, row, super-block of the step)
+    const uint8_t *tsrc[kTj];
+    uint32_t tsb[kTj], tdst[kTj];
+#pragma unroll
+    for (uint32_t j = 0; j < kTj; j++) {
+        const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
+        const uint32_t sl = qq % S, rm = qq / S;
+        tsrc[j] = row_src(rm / 16u, rm % 16u) + F::kTailSrc;
+        tsb[j] = sl;
+        tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot) : UINT32_MAX;
+    }
+    uint8_t *wl_w = &wl[wave][0];
     const uint32_t act_bytes = k_blocks * kActLdsPitch;
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
@@ -569,78 +594,75 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
         __syncthreads();
         if (!active) continue;  // wave-uniform; the block's barriers above are reached
         uint4 wv[kWj];
-        uint32_t tv = 0u;
-        auto issue = [&](uint32_t sb) {
-            const uint64_t wo = (uint64_t)sb * F::kSb;
+        uint32_t tv[kTj];
+        auto issue = [&](uint32_t step) {
 #pragma unroll
-            for (uint32_t j = 0; j < kWj; j++)
-                if (wdst[j] != UINT32_MAX) wv[j] = ldw128(wsrc[j] + wo);
-            if (t_on) tv = ldw32(tsrc + wo);
+            for (uint32_t j = 0; j < kWj; j++) {
+                const uint32_t sb = step * S + wsb[j];
+                wv[j] = ldw128(wsrc[j] + (uint64_t)(sb < k_blocks ? sb : k_blocks - 1u) * F::kSb);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kTj; j++) {
+                const uint32_t sb = step * S + tsb[j];
+                tv[j] = ldw32(tsrc[j] + (uint64_t)(sb < k_blocks ? sb : k_blocks - 1u) * F::kSb);
+            }
         };
-        // lane (pair i, kq): its pair's record, or none past the tile
-        const bool a_on = i < m;
-        const uint8_t *ar = acts_lds + (a_on ? i : 0u) * act_bytes;
+        // lane (pair i, kq): its pair's record (the last pair's past the tile)
+        const uint8_t *ar = acts_lds + (i < m ? i : m - 1u) * act_bytes;
         float acc[NM][4];
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; mt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
-        issue(0);
-        for (uint32_t sb = 0; sb < k_blocks; sb++) {
-#pragma unroll
-            for (uint32_t j = 0; j < kWj; j++)
-                if (wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
-            if (t_on) *(uint32_t *)(wl_w + tdst) = tv;
-            // the wave's own LDS slot: visible to the wave's other lanes
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (sb + 1u < k_blocks) issue(sb + 1u);  // in flight while this one is decoded
+        // super-block sb from the wave's LDS slot ws (row i of matrix 0)
+        auto sb_compute = [&](uint32_t sb, const uint8_t *ws) {
             const uint8_t *rec = ar + sb * kActLdsPitch;  // d @0, q8 values @16, bsums @272
+            // pairs past the tile read the last pair's values: their MFMA
+            // rows and sums are never stored
             float yd[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint32_t pi = 4u * kq + r;
-                yd[r] = pi < m ? *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch) : 0.0f;
+                const uint32_t pi = 4u * kq + r < m ? 4u * kq + r : m - 1u;
+                yd[r] = *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch);
             }
-            auto a_at = [&](uint32_t t) {
-                return a_on ? *(const uint2 *)(rec + 16u + 32u * t + 8u * kq) : make_uint2(0u, 0u);
-            };
+            auto a_at = [&](uint32_t t) { return *(const uint2 *)(rec + 16u + 32u * t + 8u * kq); };
             if constexpr (!kIq2) {
                 uint4 sc[NM];
                 uint2 qv[NM][2];
                 v4i isum[NM];
+                const uint32_t hsh = 8u * (kq >> 1);
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    const uint8_t *ws = wl_w + (mt * 16u + i) * kGqRowPitch;
-                    sc[mt] = *(const uint4 *)ws;
+                    const uint8_t *wm = ws + mt * 16u * kRowL;
+                    sc[mt] = *(const uint4 *)wm;
 #pragma unroll
                     for (uint32_t k = 0; k < 2; k++)
-                        qv[mt][k] = *(const uint2 *)(ws + 16u + 32u * k + 16u * (kq >> 1) + 8u * (kq & 1u));
+                        qv[mt][k] = *(const uint2 *)(wm + 16u + 32u * k + 16u * (kq >> 1) + 8u * (kq & 1u));
                     isum[mt] = v4i{0, 0, 0, 0};
                 }
 #pragma unroll
                 for (uint32_t t = 0; t < 8; t++) {
                     const uint2 a = a_at(t);
-                    const uint32_t sbi = 2u * t + (kq >> 1);  // sub-block
                     const uint32_t sh = 2u * (t & 3u);
 #pragma unroll
                     for (uint32_t mt = 0; mt < NM; mt++) {
+                        // scales of sub-blocks 2t + kq / 2 (t even: byte kq / 2 of
+                        // scale word t / 2, t odd: byte kq / 2 + 2), as both
+                        // 16-bit halves of s2
                         const uint32_t scw[4] = {sc[mt].x, sc[mt].y, sc[mt].z, sc[mt].w};
-                        const uint32_t scv = (scw[sbi >> 2] >> (8u * (sbi & 3u))) & 0x0fu;
-                        const uint32_t tab = __umul24(scv, 0x030201u) << 8;  // {0, sc, 2sc, 3sc}
+                        const uint32_t pr2 = (scw[t >> 1] >> hsh) & 0x000f000fu;
+                        const uint32_t s2 = __builtin_amdgcn_perm(0u, pr2, (t & 1u) ? 0x0C020C02u : 0x0C000C00u);
+                        // codes (0..3 per byte) times the scale, per 16-bit half:
+                        // c0 sc + 256 c1 sc with c sc <= 45, so no carry between bytes
                         const uint2 q = qv[mt][t >> 2];
-                        const uint2 b = make_uint2(__builtin_amdgcn_perm(0u, tab, (q.x >> sh) & 0x03030303u),
-                                                   __builtin_amdgcn_perm(0u, tab, (q.y >> sh) & 0x03030303u));
+                        const uint2 b = make_uint2(pk_mul16((q.x >> sh) & 0x03030303u, s2),
+                                                   pk_mul16((q.y >> sh) & 0x03030303u, s2));
                         isum[mt] = mfma16x16x32(a, b, isum[mt]);
                     }
                 }
                 // lane (pair i, kq): l (kq < 2) or h (kq >= 2) bytes of bsums 8 (kq & 1) + [0, 8)
-                uint2 alh = make_uint2(0u, 0u);
-                if (a_on) {
-                    const uint4 bs = *(const uint4 *)(rec + 272u + 16u * (kq & 1u));
-                    alh = make_uint2(bsum_bytes(bs.x, bs.y, kq >= 2u), bsum_bytes(bs.z, bs.w, kq >= 2u));
-                }
+                const uint4 bs = *(const uint4 *)(rec + 272u + 16u * (kq & 1u));
+                const uint2 alh = make_uint2(bsum_bytes(bs.x, bs.y, kq >= 2u), bsum_bytes(bs.z, bs.w, kq >= 2u));
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
                     // mins of sub-blocks 8 (kq & 1) + [0, 8) against l (kq < 2) and h (kq >= 2)
@@ -649,7 +671,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                     const uint2 zero = make_uint2(0u, 0u);
                     const v4i dl = mfma16x16x32(alh, kq < 2u ? mn : zero);
                     const v4i dh = mfma16x16x32(alh, kq < 2u ? zero : mn);
-                    const uint32_t dd = *(const uint32_t *)(wl_w + (mt * 16u + i) * kGqRowPitch + F::kTailSlot);
+                    const uint32_t dd = *(const uint32_t *)(ws + mt * 16u * kRowL + F::kTailSlot);
                     const float xd = f16f((uint16_t)dd), xmin = f16f((uint16_t)(dd >> 16));
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
@@ -663,12 +685,15 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                 for (uint32_t mt = 0; mt < NM; mt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) bsum[mt][r] = 0;
-#pragma unroll
+#ifndef PK_GQ_IQ2_UNROLL
+#define PK_GQ_IQ2_UNROLL 4
+#endif
+#pragma unroll PK_GQ_IQ2_UNROLL
                 for (uint32_t g = 0; g < 8; g++) {
                     const uint2 a = a_at(g);
 #pragma unroll
                     for (uint32_t mt = 0; mt < NM; mt++) {
-                        const uint2 aux = *(const uint2 *)(wl_w + (mt * 16u + i) * kGqRowPitch + 8u * g);
+                        const uint2 aux = *(const uint2 *)(ws + mt * 16u * kRowL + 8u * g);
                         uint2 b;
                         iq2_signed8(lut, (aux.x >> (8u * kq)) & 0xffu, (aux.y >> (7u * kq)) & 127u, b.x, b.y);
                         const v4i d = mfma16x16x32(a, b);
@@ -679,12 +704,29 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                 }
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    const float xd = f16f(*(const uint16_t *)(wl_w + (mt * 16u + i) * kGqRowPitch + F::kTailSlot));
+                    const float xd = f16f(*(const uint16_t *)(ws + mt * 16u * kRowL + F::kTailSlot));
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[mt][r] += 0.125f * xd * yd[r] * (float)bsum[mt][r];
                 }
             }
-            // this super-block's LDS reads are consumed before the next copy
+        };
+        issue(0);
+        for (uint32_t step = 0; step < n_steps; step++) {
+#pragma unroll
+            for (uint32_t j = 0; j < kWj; j++)
+                if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
+#pragma unroll
+            for (uint32_t j = 0; j < kTj; j++)
+                if ((j + 1u) * 64u <= kTp || tdst[j] != UINT32_MAX) *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+            // the wave's own LDS slots: visible to the wave's other lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            issue(step + 1u < n_steps ? step + 1u : n_steps - 1u);  // in flight while this step is decoded
+#pragma unroll
+            for (uint32_t sl = 0; sl < S; sl++)
+                if (step * S + sl < k_blocks) sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot);
+            // this step's LDS reads are consumed before the next copy
             __builtin_amdgcn_wave_barrier();
         }
         // lane (row i, kq): pairs 4kq + r of the tile
