@@ -1,19 +1,21 @@
-// mmq.hip - dense matvec for token chunks (5..16 tokens per tile) on the
-// int8 matrix cores: v_mfma_i32_16x16x64_i8.
+// mmq.hip - int8 matrix-core (v_mfma_i32_16x16x32_i8) kernels:
+//   mmq_kernel: the dense Q6_K matvec for token chunks (5..16 tokens per
+//     tile). A block computes 16 RT weight rows x 16 tokens; its NW waves
+//     split the row's super-blocks (split-K) and the partials are added in
+//     wave order through LDS (deterministic);
+//   moe_grouped_mmq_kq_kernel: the grouped MoE stages (16 rows x up to 16
+//     (token, slot) pairs of one expert per MFMA tile) for Q2_K, IQ2_XXS and
+//     MXFP4 experts.
+// Every kernel produces exact int32 group sums with MFMA, applies the
+// format's integer scales in int32, forms the per-super-block fp32 value in
+// the reference's operation order and accumulates super-blocks in order.
 //
-// A block computes 16 RT weight rows x 16 tokens. Its NW waves split the
-// row's super-blocks (split-K); every wave produces exact int32 group sums
-// with MFMA, applies the format's integer scales in int32, forms the per-
-// super-block fp32 value in the reference's operation order, accumulates its
-// super-blocks in order, and the NW partials are added in wave order through
-// LDS (deterministic).
-//
-// Operand layout of v_mfma_i32_16x16x64_i8 (16 int8 per lane):
+// Operand layout of v_mfma_i32_16x16x32_i8 (8 int8 per lane):
 //   A[i][k]: lane i + 16 * kq, K slots of lane group kq
 //   B[k][j]: lane j + 16 * kq, the same K slots
 //   D[i][j]: lane j + 16 * (i / 4), element i % 4
-// Which 16 slots a lane group holds does not matter here: A and B hold the
-// same ones, and every sum below is over whole lane groups.
+// Which 8 slots a lane group holds does not matter: A and B hold the same
+// ones, and every sum is over whole lane groups.
 #include "pk_rowdot.h"
 #include "pk_route.h"
 
@@ -246,202 +248,7 @@ int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_
     }
 }
 
-// ------------------------------------------------- grouped MXFP4 (MoE) --
-// One block per (16-row tile, expert group); the group's (token, slot)
-// pairs are taken 16 at a time. Per 32-value block one
-// v_mfma_i32_16x16x32_i8 gives the exact block sums for 16 pairs x 16 rows:
-// A = the pairs' q8 values, B = the rows' E2M1 codes doubled to int8. Lane
-// group kq holds values {0, 16, 8, 24}[kq] + [0, 8) of the block: nibble
-// kq & 1 of qs bytes 8 (kq >> 1) .. + 7. The 4 waves take contiguous ranges
-// of the row's super-blocks. Per super-block a wave copies the 16 rows'
-// blocks (one 17-byte block per lane: a wave-wide load covers 8 rows x 136
-// contiguous bytes; qs to 16-byte aligned slots, e apart) and the 16 pairs'
-// q8 values (a wave-wide load covers 4 pairs x 256 bytes) into its own LDS
-// area, so every global load is contiguous and every MFMA operand is an
-// aligned LDS read. Per (row, pair) and in block order the reference's
-// sumf += scale_half(e) * sumi for sumi != 0, then row += yd * sumf per
-// super-block (pulsar_kernels.cu:5715-5741) in the wave's range; the
-// block adds the 4 ranges in order.
-constexpr uint32_t kMmqPairs = 16;
-
-template <bool PAIR>
-__global__ __launch_bounds__(256) void moe_grouped_mmq_mxfp4_kernel(
-        float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
-        const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
-        const pulsar_block_q8_K *__restrict__ act, uint32_t k_dim, uint32_t k_blocks, uint32_t n_rows,
-        uint32_t n_used, uint64_t row_bytes, uint32_t act_op) {
-    constexpr uint32_t NM = PAIR ? 2 : 1;
-    // rows / pairs padded by 16 bytes: the 16 rows (pairs) an MFMA operand
-    // read touches fall in distinct LDS banks
-    __shared__ __align__(16) uint4 wq_l[4][NM][16][9];    // [wave][matrix][row][block] qs
-    __shared__ __align__(8) uint8_t we_l[4][NM][16][8];   // e
-    __shared__ __align__(16) uint4 aq_l[4][16][17];       // [wave][pair][16-byte piece] q8 values
-    __shared__ float part[4][NM][16][17];                 // [wave][matrix][row][pair]
-    __shared__ uint32_t pr_l[kMmqPairs];
-    const uint32_t group = blockIdx.y;
-    const pulsar_expert_ptrs p = gptrs[group];
-    const uint8_t *w0 = PAIR ? (const uint8_t *)p.gate : (const uint8_t *)p.down;
-    const uint8_t *w1 = PAIR ? (const uint8_t *)p.up : nullptr;
-    if (!w0 || (PAIR && !w1)) return;
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
-    if (s0 >= s1) return;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t i = lane & 15u, kq = lane >> 4;
-    const uint32_t row0 = blockIdx.x * 16u;
-    // weight copy lanes: block lane & 7 of rows lane >> 3 and 8 + (lane >> 3)
-    const uint32_t cb = lane & 7u, cr = lane >> 3;
-    const uint8_t *cp[NM][2];  // block b of the row: e at 17b, qs at 17b + 1
-#pragma unroll
-    for (uint32_t h = 0; h < 2; h++) {
-        const uint32_t r = row0 + cr + 8u * h;
-        const uint64_t ro = (uint64_t)(r < n_rows ? r : n_rows - 1u) * row_bytes;
-        cp[0][h] = as_global(w0) + ro;
-        if (PAIR) cp[NM - 1][h] = as_global(w1) + ro;
-    }
-    const uint32_t nsh = 4u * (kq & 1u);
-    const uint32_t a_piece = (kq >> 1) + 2u * (kq & 1u);  // 8-byte piece of a 32-value block: 0, 2, 1, 3
-    const uint32_t nblk32 = k_dim / 32u;
-    const uint32_t per = (k_blocks + 3u) / 4u;
-    const uint32_t sb_lo = wave * per, sb_hi = sb_lo + per < k_blocks ? sb_lo + per : k_blocks;
-    for (uint32_t t0 = s0; t0 < s1; t0 += kMmqPairs) {
-        const uint32_t m = s1 - t0 < kMmqPairs ? s1 - t0 : kMmqPairs;
-        if (t0 != s0) __syncthreads();  // the previous tile's partials are consumed
-        if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
-        __syncthreads();
-        // activation copy lanes: piece lane & 15 of pairs lane >> 4 + 4j
-        const uint8_t *ap[4];
-#pragma unroll
-        for (uint32_t j = 0; j < 4; j++) {
-            const uint32_t pi = (lane >> 4) + 4u * j;
-            const uint32_t pr = pr_l[pi < m ? pi : 0u];
-            ap[j] = (const uint8_t *)(act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) *
-                                                k_blocks) + 4u + 16u * (lane & 15u);
-        }
-        const uint8_t *drow[4];  // yd of pairs 4kq + r
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t pi = 4u * kq + r;
-            const uint32_t pr = pr_l[pi < m ? pi : 0u];
-            drow[r] = (const uint8_t *)(act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) *
-                                                  k_blocks);
-        }
-        float acc[NM][4];
-#pragma unroll
-        for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
-        for (uint32_t sb = sb_lo; sb < sb_hi; sb++) {
-            const uint32_t b0 = sb * 8u, nb = nblk32 - b0 < 8u ? nblk32 - b0 : 8u;
-            // copy the super-block's 16 rows (clamped: never past the row)
-            const uint64_t co = 17ull * (b0 + (cb < nb ? cb : 0u));
-            uint4 q[NM][2];
-            uint32_t e[NM][2];
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-                for (uint32_t h = 0; h < 2; h++) {
-                    q[mt][h] = ldw128(cp[mt][h] + co + 1u);
-                    e[mt][h] = ldw8(cp[mt][h] + co);
-                }
-            uint4 av[4];
-#pragma unroll
-            for (uint32_t j = 0; j < 4; j++) av[j] = ld128(ap[j] + (uint64_t)sb * 292u);
-            float yd[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) yd[r] = __builtin_bit_cast(float, ld32(drow[r] + (uint64_t)sb * 292u));
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-                for (uint32_t h = 0; h < 2; h++) {
-                    wq_l[wave][mt][cr + 8u * h][cb] = q[mt][h];
-                    we_l[wave][mt][cr + 8u * h][cb] = (uint8_t)e[mt][h];
-                }
-#pragma unroll
-            for (uint32_t j = 0; j < 4; j++) {
-                const uint32_t pi = (lane >> 4) + 4u * j;
-                aq_l[wave][pi][lane & 15u] = pi < m ? av[j] : make_uint4(0u, 0u, 0u, 0u);
-            }
-            // the wave's own LDS area: visible to the wave's other lanes
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            float f[NM][4];
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) f[mt][r] = 0.0f;
-            uint2 ev[NM];
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; mt++) ev[mt] = *(const uint2 *)&we_l[wave][mt][i][0];
-#pragma unroll
-            for (uint32_t bl = 0; bl < 8; bl++) {
-                if (bl >= nb) break;  // uniform
-                const uint2 a = *((const uint2 *)&aq_l[wave][i][0] + 4u * bl + a_piece);
-#pragma unroll
-                for (uint32_t mt = 0; mt < NM; mt++) {
-                    const uint2 qq = *((const uint2 *)&wq_l[wave][mt][i][bl] + (kq >> 1));
-                    const uint2 c = make_uint2(mxfp4_kv4(qq.x >> nsh), mxfp4_kv4(qq.y >> nsh));
-                    const v4i d = mfma16x16x32(a, c);
-                    const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
-                    // = the reference's `if (sumi != 0) sumf += sc * sumi`: sc
-                    // is 0 or a power of two and |sumi| < 2^24, so sc * sumi is
-                    // exact and one fma rounds like the multiply-add; a zero
-                    // sumi adds +0, which leaves sumf (never -0) unchanged
-#pragma unroll
-                    for (int r = 0; r < 4; r++) f[mt][r] = __builtin_fmaf(sc, (float)d[r], f[mt][r]);
-                }
-            }
-#pragma unroll
-            for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[mt][r] += yd[r] * f[mt][r];
-        }
-#pragma unroll
-        for (uint32_t mt = 0; mt < NM; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) part[wave][mt][i][4u * kq + r] = acc[mt][r];
-        __syncthreads();
-        // one thread per (row, pair): the 4 ranges in order, then the epilogue
-        const uint32_t ri = threadIdx.x & 15u, pi = threadIdx.x >> 4;
-        if (pi < m && row0 + ri < n_rows) {
-            const float g = ((part[0][0][ri][pi] + part[1][0][ri][pi]) + part[2][0][ri][pi]) + part[3][0][ri][pi];
-            const uint32_t pr = pr_l[pi];
-            const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-            const uint32_t orow = row0 + ri;
-            if (PAIR) {
-                float u = ((part[0][NM - 1][ri][pi] + part[1][NM - 1][ri][pi]) + part[2][NM - 1][ri][pi]) +
-                          part[3][NM - 1][ri][pi];
-                float gg = g;
-                if (p.gate_b) gg += ldwf(p.gate_b + orow);
-                if (p.up_b) u += ldwf(p.up_b + orow);
-                out[so * n_rows + orow] = glu(gg, u, act_op) * weights[so];
-            } else {
-                out[so * n_rows + orow] = g;
-            }
-        }
-    }
-}
-
-// Grouped MoE stages of MXFP4 experts on the matrix cores (pair: gate/up +
-// combine into mid; down: per-pair partials). Returns the launch status.
-int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const void *starts, const void *pairs,
-                             const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
-                             uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
-    const uint32_t k_blocks = (k_dim + 255u) / 256u;
-    const dim3 grid((n_rows + 15u) / 16u, n_group);
-    const size_t lds = 0;
-    if (pair)
-        hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<true>, grid, dim3(256), lds, pk::stream(), out,
-                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
-                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op);
-    else
-        hipLaunchKernelGGL(moe_grouped_mmq_mxfp4_kernel<false>, grid, dim3(256), lds, pk::stream(), out,
-                           (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs,
-                           weights, act, k_dim, k_blocks, n_rows, n_used, row_bytes, act_op);
-    return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
-}
-
-// ----------------------------------------- grouped Q2_K / IQ2_XXS (MoE) --
+// ------------------------------------ grouped Q2_K / IQ2_XXS / MXFP4 (MoE) --
 // Block = 64 rows (16 per wave) x up to kGqPairs pairs of one expert group,
 // the whole K per wave (no split). The pairs' q8_K rows are staged in LDS
 // once per pair tile (load_act_lds layout); each wave streams its 16 rows
@@ -468,23 +275,44 @@ int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const voi
 // value is then complete (no cross-wave sum).
 template <uint32_t Q>
 struct GmmqFmt;
+// Row super-block copies: kPieces 16-byte pieces (piece_off) to slot 16c,
+// kTails small loads (tail_off, kTailBytes each) to kTailSlot + c. `lim`
+// bounds the clamped unit (super-blocks, or 32-blocks for MXFP4).
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q2_K> {
-    static constexpr uint32_t kSb = 84;
-    static constexpr uint32_t kPieces = 5;     // 16-byte copies: bytes 0..79 to slot 0..79
-    static constexpr uint32_t kSrc0 = 0;       // first copied byte
-    static constexpr uint32_t kTailSrc = 80;   // d, dmin (4 bytes) ...
-    static constexpr uint32_t kTailSlot = 80;  // ... to slot 80
+    static constexpr uint32_t kPieces = 5, kTails = 1, kTailBytes = 4;
+    static constexpr uint32_t kTailSlot = 80;  // d, dmin
     static constexpr uint32_t kSlot = 96;      // LDS bytes per row super-block
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        return (sb < lim ? sb : lim - 1u) * 84u + 16u * c;  // scales, qs: bytes 0..79
+    }
+    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t, uint32_t lim) { return (sb < lim ? sb : lim - 1u) * 84u + 80u; }
 };
 template <>
 struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
-    static constexpr uint32_t kSb = 66;
-    static constexpr uint32_t kPieces = 4;     // bytes 2..65 (the groups) to slot 0..63
-    static constexpr uint32_t kSrc0 = 2;
-    static constexpr uint32_t kTailSrc = 0;    // d (read as 4 bytes, the upper 2 unused) ...
-    static constexpr uint32_t kTailSlot = 64;  // ... to slot 64
+    static constexpr uint32_t kPieces = 4, kTails = 1, kTailBytes = 4;
+    static constexpr uint32_t kTailSlot = 64;  // d (the upper 2 bytes unused)
     static constexpr uint32_t kSlot = 80;
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        return (sb < lim ? sb : lim - 1u) * 66u + 2u + 16u * c;  // the 8 groups: bytes 2..65
+    }
+    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t, uint32_t lim) { return (sb < lim ? sb : lim - 1u) * 66u; }
+};
+template <>
+struct GmmqFmt<PULSAR_QUANT_MXFP4> {
+    // super-block = 8 blocks of 17 bytes; block c's qs to slot 16c, its e
+    // to slot 128 + c
+    static constexpr uint32_t kPieces = 8, kTails = 8, kTailBytes = 1;
+    static constexpr uint32_t kTailSlot = 128;
+    static constexpr uint32_t kSlot = 144;
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        const uint32_t b = 8u * sb + c;
+        return 17u * (b < lim ? b : lim - 1u) + 1u;
+    }
+    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        const uint32_t b = 8u * sb + c;
+        return 17u * (b < lim ? b : lim - 1u);
+    }
 };
 #ifndef PK_GQ_SBS
 #define PK_GQ_SBS 2u
@@ -495,6 +323,10 @@ struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
 constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy step
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
+#ifndef PK_GQ_ACT_LDS_MX
+#define PK_GQ_ACT_LDS_MX 40960u
+#endif
+constexpr uint32_t kGqActLdsMx = PK_GQ_ACT_LDS_MX;  // the same for MXFP4 experts
 
 // Per 16-bit half: a * b (low 16 bits), one v_pk_mul_lo_u16
 typedef unsigned short pk_ushort2 __attribute__((ext_vector_type(2)));
@@ -519,16 +351,17 @@ template <uint32_t Q, bool PAIR>
 __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
         float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
         const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
-        const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t n_rows, uint32_t n_used,
-        uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
+        const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t lim, uint32_t n_rows,
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
     using F = GmmqFmt<Q>;
     constexpr uint32_t NM = PAIR ? 2 : 1;
     constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
-    constexpr uint32_t S = kGqSbs;
+    constexpr bool kMx = Q == PULSAR_QUANT_MXFP4;
+    constexpr uint32_t S = kMx ? 1u : kGqSbs;  // an MXFP4 super-block row is 136 contiguous bytes already
     constexpr uint32_t kRowL = S * F::kSlot + 16u;        // LDS bytes per row (S slots, padded)
     constexpr uint32_t kWp = NM * 16u * S * F::kPieces;  // weight pieces per step
     constexpr uint32_t kWj = (kWp + 63u) / 64u;         // ... per lane
-    constexpr uint32_t kTp = NM * 16u * S;              // tails per step
+    constexpr uint32_t kTp = NM * 16u * S * F::kTails;  // tails per step
     constexpr uint32_t kTj = (kTp + 63u) / 64u;
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint2 lut[kIq2 ? kIq2LutRows : 1];
@@ -560,25 +393,25 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     // blocks. Lanes past the last piece load one too (never stored), so
     // every lane issues the same loads and the waits count them exactly.
     const uint8_t *wsrc[kWj];
-    uint32_t wsb[kWj], wdst[kWj];
+    uint32_t wsc[kWj], wdst[kWj];  // wsc = slot << 8 | piece
 #pragma unroll
     for (uint32_t j = 0; j < kWj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kWp ? q : kWp - 1u;
         const uint32_t c = qq % F::kPieces, rs = qq / F::kPieces, sl = rs % S, rm = rs / S;
-        wsrc[j] = row_src(rm / 16u, rm % 16u) + F::kSrc0 + 16u * c;
-        wsb[j] = sl;
+        wsrc[j] = row_src(rm / 16u, rm % 16u);
+        wsc[j] = sl << 8 | c;
         wdst[j] = q < kWp ? (rm * kRowL + sl * F::kSlot + 16u * c) : UINT32_MAX;
     }
-    // tails (d / dmin): one per (matrix, row, super-block of the step)
+    // tails (d / dmin, MXFP4 e): kTails per (matrix, row, super-block of the step)
     const uint8_t *tsrc[kTj];
-    uint32_t tsb[kTj], tdst[kTj];
+    uint32_t tsc[kTj], tdst[kTj];
 #pragma unroll
     for (uint32_t j = 0; j < kTj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
-        const uint32_t sl = qq % S, rm = qq / S;
-        tsrc[j] = row_src(rm / 16u, rm % 16u) + F::kTailSrc;
-        tsb[j] = sl;
-        tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot) : UINT32_MAX;
+        const uint32_t c = qq % F::kTails, rs = qq / F::kTails, sl = rs % S, rm = rs / S;
+        tsrc[j] = row_src(rm / 16u, rm % 16u);
+        tsc[j] = sl << 8 | c;
+        tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot + c) : UINT32_MAX;
     }
     uint8_t *wl_w = &wl[wave][0];
     const uint32_t act_bytes = k_blocks * kActLdsPitch;
@@ -597,14 +430,12 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
         uint32_t tv[kTj];
         auto issue = [&](uint32_t step) {
 #pragma unroll
-            for (uint32_t j = 0; j < kWj; j++) {
-                const uint32_t sb = step * S + wsb[j];
-                wv[j] = ldw128(wsrc[j] + (uint64_t)(sb < k_blocks ? sb : k_blocks - 1u) * F::kSb);
-            }
+            for (uint32_t j = 0; j < kWj; j++)
+                wv[j] = ldw128(wsrc[j] + F::piece_off(step * S + (wsc[j] >> 8), wsc[j] & 0xffu, lim));
 #pragma unroll
             for (uint32_t j = 0; j < kTj; j++) {
-                const uint32_t sb = step * S + tsb[j];
-                tv[j] = ldw32(tsrc[j] + (uint64_t)(sb < k_blocks ? sb : k_blocks - 1u) * F::kSb);
+                const uint8_t *tp = tsrc[j] + F::tail_off(step * S + (tsc[j] >> 8), tsc[j] & 0xffu, lim);
+                tv[j] = F::kTailBytes == 4u ? ldw32(tp) : ldw8(tp);
             }
         };
         // lane (pair i, kq): its pair's record (the last pair's past the tile)
@@ -626,7 +457,40 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                 yd[r] = *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch);
             }
             auto a_at = [&](uint32_t t) { return *(const uint2 *)(rec + 16u + 32u * t + 8u * kq); };
-            if constexpr (!kIq2) {
+            if constexpr (kMx) {
+                // lane group kq: values {0, 16, 8, 24}[kq] + [0, 8) of a block,
+                // nibble kq & 1 of qs bytes 8 (kq >> 1) + [0, 8); per block the
+                // reference's sumf += scale_half(e) * sumi for sumi != 0 (an fma
+                // of a power of two and an int < 2^24 is exact, and sumi = 0
+                // adds +0 to a sum that is never -0), then yd * sumf
+                const uint32_t nsh = 4u * (kq & 1u), a_piece = (kq >> 1) + 2u * (kq & 1u);
+                const uint32_t nb = lim - 8u * sb < 8u ? lim - 8u * sb : 8u;
+                uint2 ev[NM];
+                float f[NM][4];
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    ev[mt] = *(const uint2 *)(ws + mt * 16u * kRowL + F::kTailSlot);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) f[mt][r] = 0.0f;
+                }
+#pragma unroll
+                for (uint32_t bl = 0; bl < 8; bl++) {
+                    if (bl >= nb) break;  // uniform: the row's last super-block may be short
+                    const uint2 a = *(const uint2 *)(rec + 16u + 32u * bl + 8u * a_piece);
+#pragma unroll
+                    for (uint32_t mt = 0; mt < NM; mt++) {
+                        const uint2 qq = *(const uint2 *)(ws + mt * 16u * kRowL + 16u * bl + 8u * (kq >> 1));
+                        const v4i d = mfma16x16x32(a, make_uint2(mxfp4_kv4(qq.x >> nsh), mxfp4_kv4(qq.y >> nsh)));
+                        const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
+#pragma unroll
+                        for (int r = 0; r < 4; r++) f[mt][r] = __builtin_fmaf(sc, (float)d[r], f[mt][r]);
+                    }
+                }
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[mt][r] += yd[r] * f[mt][r];
+            } else if constexpr (!kIq2) {
                 uint4 sc[NM];
                 uint2 qv[NM][2];
                 v4i isum[NM];
@@ -716,8 +580,13 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
             for (uint32_t j = 0; j < kWj; j++)
                 if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
 #pragma unroll
-            for (uint32_t j = 0; j < kTj; j++)
-                if ((j + 1u) * 64u <= kTp || tdst[j] != UINT32_MAX) *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+            for (uint32_t j = 0; j < kTj; j++) {
+                if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
+                if (F::kTailBytes == 4u)
+                    *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+                else
+                    wl_w[tdst[j]] = (uint8_t)tv[j];
+            }
             // the wave's own LDS slots: visible to the wave's other lanes
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -751,31 +620,39 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     }
 }
 
-// Grouped MoE stages of Q2_K / IQ2_XXS experts on the matrix cores; -1 for
-// other formats (the caller then uses the lane kernels).
+// Grouped MoE stages of Q2_K / IQ2_XXS / MXFP4 experts on the matrix cores;
+// -1 for other formats (the caller then uses the lane kernels).
 int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
                           const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
                           uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
-    if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS) return -1;
-    const uint32_t k_blocks = k_dim / 256u;
+    if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS && quant != PULSAR_QUANT_MXFP4) return -1;
+    const uint32_t k_blocks = (k_dim + 255u) / 256u;
+    const uint32_t lim = quant == PULSAR_QUANT_MXFP4 ? k_dim / 32u : k_blocks;
     const uint32_t per_pair = k_blocks * kActLdsPitch;
-    if (per_pair > kGqActLds) return -1;  // one pair's row does not fit: lane kernels
-    uint32_t pmax = kGqActLds / per_pair;
+    // MXFP4 layers route many pairs to each expert (gpt-oss: 64 tokens x 4 of
+    // 32 experts), so their tiles take more pairs per weight pass
+    const uint32_t budget = quant == PULSAR_QUANT_MXFP4 ? kGqActLdsMx : kGqActLds;
+    if (per_pair > budget) return -1;  // one pair's row does not fit: lane kernels
+    uint32_t pmax = budget / per_pair;
     pmax = pmax < kGqPairs ? pmax : kGqPairs;
     const size_t lds = (size_t)pmax * per_pair;
     const dim3 grid((n_rows + 63u) / 64u, n_group);
 #define PK_GQ(Q, P)                                                                                              \
     hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P>), grid, dim3(256), lds, pk::stream(), out,             \
                        (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs, weights, \
-                       act, k_blocks, n_rows, n_used, row_bytes, act_op, pmax)
+                       act, k_blocks, lim, n_rows, n_used, row_bytes, act_op, pmax)
     if (quant == PULSAR_QUANT_Q2_K && pair)
         PK_GQ(PULSAR_QUANT_Q2_K, true);
     else if (quant == PULSAR_QUANT_Q2_K)
         PK_GQ(PULSAR_QUANT_Q2_K, false);
-    else if (pair)
+    else if (quant == PULSAR_QUANT_IQ2_XXS && pair)
         PK_GQ(PULSAR_QUANT_IQ2_XXS, true);
-    else
+    else if (quant == PULSAR_QUANT_IQ2_XXS)
         PK_GQ(PULSAR_QUANT_IQ2_XXS, false);
+    else if (pair)
+        PK_GQ(PULSAR_QUANT_MXFP4, true);
+    else
+        PK_GQ(PULSAR_QUANT_MXFP4, false);
 #undef PK_GQ
     return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
 }

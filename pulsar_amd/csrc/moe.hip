@@ -7,10 +7,11 @@
 //   down : one block per (row group, token); the block's 4 waves split the
 //          token's slots, each slot's row dot lands in LDS and the slots
 //          are summed in slot order.
-// Grouped path (CSR by expert, pulsar_kernels.cu:2689-2789): one block per
-// (row block, expert group); the group's pair activations are staged in LDS
-// once, and each wave streams row passes of the expert (the next pass's
-// weights in flight while the current one is dotted with every pair).
+// Grouped path (CSR by expert, pulsar_kernels.cu:2689-2789): Q2_K, IQ2_XXS
+// and MXFP4 experts run on the int8 matrix cores (mmq.hip); Q4_K / Q6_K
+// experts here, one block per (row block, expert group): the group's pair
+// activations are staged in LDS once, and each wave streams row passes of
+// the expert, dotting each pass with every pair.
 #include "pk_rowdot.h"
 
 namespace pk {
@@ -460,11 +461,8 @@ extern "C" int pulsar_moe_down(void *out, const void *ptrs, const void *midq, ui
 // (pulsar_kernels.cu:3488-3492, 3541-3547): in_dim (pair) and mid_dim (down)
 // multiples of 256, n_used <= 16 (4-bit slot field in `pairs`).
 namespace pk {
-// mmq.hip: the grouped stages of MXFP4 experts on the matrix cores
-int launch_grouped_mmq_mxfp4(bool pair, float *out, const void *gptrs, const void *starts, const void *pairs,
-                             const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows,
-                             uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
-// mmq.hip: the same for Q2_K / IQ2_XXS experts; -1 for other formats
+// mmq.hip: the grouped stages of Q2_K / IQ2_XXS / MXFP4 experts on the
+// matrix cores; -1 for other formats
 int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
                           const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
                           uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
@@ -486,10 +484,6 @@ extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, cons
         n_group > 65535u || row_bytes == 0 ||
         (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI))
         return reject("moe pair swiglu grouped");
-    if (quant == PULSAR_QUANT_MXFP4)
-        return launch_grouped_mmq_mxfp4(true, (float *)mid, gptrs, starts, pairs, (const float *)weights,
-                                        (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group, row_bytes,
-                                        act_op);
 #ifndef PK_GRP_LANE_ONLY
     {
         const int r = launch_grouped_mmq_kq(true, quant, (float *)mid, gptrs, starts, pairs, (const float *)weights,
@@ -514,10 +508,6 @@ extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const v
         out_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 || n_group > 65535u ||
         row_bytes == 0)
         return reject("moe down grouped");
-    if (quant == PULSAR_QUANT_MXFP4)
-        return launch_grouped_mmq_mxfp4(false, (float *)partial, gptrs, starts, pairs, nullptr,
-                                        (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
-                                        row_bytes, 0);
 #ifndef PK_GRP_LANE_ONLY
     {
         const int r = launch_grouped_mmq_kq(false, quant, (float *)partial, gptrs, starts, pairs, nullptr,

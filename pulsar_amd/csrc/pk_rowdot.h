@@ -123,8 +123,9 @@ template <uint32_t Q, uint32_t UPLMAX>
 PK_DEV void load_row_w(const uint8_t *row, const RowGeom &rg, typename Fmt<Q>::W (&w)[UPLMAX]) {
 #pragma unroll
     for (uint32_t i = 0; i < UPLMAX; i++) {
+        // no branch around the loads, not even a uniform one: every call
+        // issues the same loads, so the waits that follow count exactly
         const uint32_t g = rg.lir + (i << rg.lpr_log2);
-        if ((i << rg.lpr_log2) >= rg.n_units) continue;  // uniform
         w[i] = Fmt<Q>::load(row, g < rg.n_units ? g : rg.n_units - 1u, rg.nblk32);
     }
 }
