@@ -187,8 +187,11 @@ class DevLayer:
 
 def bench_moe(ctx, spec, steps, warmup, path: str):
     """One whole layer per step. path: "plain" (reference entry points with
-    device routing), "grouped" (CSR by expert, grouped kernels) or "fused"
-    (router_logits_q8 + moe_pair_routed + moe_down_f32: three launches)."""
+    device routing), "grouped" (router_logits_q8 + moe_route_group + the
+    grouped stages + moe_slot_sum[_bias]: six launches), "grouped_split"
+    (the same grouped stages behind the reference's separate router, select,
+    pointer and CSR entry points: nine or ten) or "fused" (router_logits_q8 +
+    moe_pair_routed + moe_down_f32: three launches)."""
     torch, K, fm = ctx["torch"], ctx["K"], ctx["fm"]
     s = spec
     bank_bytes = s.n_expert * s.expert_bytes
@@ -230,6 +233,20 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
             K.moe_down_f32(out, ptrs, slot_w, mid, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
                            s.down_quant, s.biases)
             return
+        if path == "grouped":
+            K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+            K.moe_route_group(sel, rw, ptrs, slot_w, gptrs, starts, pairs, logits, None, s.n_expert, s.k_used, 1.0,
+                              1, descs[i % n_banks], shared[i % n_banks] if shared else None, s.n_tok, max_groups)
+            K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq, s.hidden, s.ffn, n_slots,
+                                      max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+            K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
+            K.moe_down_grouped(partial, gptrs, starts, pairs, midq, s.ffn, s.hidden, n_slots, max_groups,
+                               s.down_row_bytes, s.down_quant)
+            if s.biases:
+                K.moe_slot_sum_bias(out, partial, ptrs, slot_w, s.hidden, n_slots, s.n_tok)
+            else:
+                K.moe_slot_sum(out, partial, s.hidden, n_slots, s.n_tok)
+            return
         K.matmul_f32(logits, b["router_w"], x, s.hidden, s.n_expert, s.n_tok)
         if b["router_b"] is not None:
             K.add_bias_rows(logits, b["router_b"], s.n_expert, s.n_tok)
@@ -237,7 +254,7 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
         K.moe_route_ptrs(ptrs, slot_w, sel, rw, descs[i % n_banks], s.n_expert,
                          shared[i % n_banks] if shared else None, s.n_tok, s.k_used)
         K.quantize_q8_k(xq, x, s.hidden, s.n_tok)
-        if path == "grouped":
+        if path == "grouped_split":
             K.moe_group_csr(gptrs, starts, pairs, ptrs, s.n_tok, n_slots, max_groups)
             K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq, s.hidden, s.ffn, n_slots,
                                       max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
@@ -425,6 +442,8 @@ def main():
         # the same layer through the reference's own (unfused) entry points
         if path == "fused" and on(spec.name + "_unfused"):
             results[spec.name + "_unfused"] = bench_moe(ctx, spec, layer_steps, warmup, "plain")
+        if spec is synth.C4_Q2K and on(spec.name + "_split"):
+            results[spec.name + "_split"] = bench_moe(ctx, spec, layer_steps, warmup, "grouped_split")
     peak = stream_peak(ctx) if want is None else None
 
     head = results.get(HEADLINE) or next(iter(results.values()))

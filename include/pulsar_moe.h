@@ -202,6 +202,29 @@ int pulsar_moe_route_ptrs(void *ptrs, void *slot_weights, const void *selected,
 int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, const void *ptrs,
                          uint32_t n_tok, uint32_t n_used, uint32_t max_groups);
 
+/* pulsar_router_select (softmax_mode 0 or 1, no sink slots) +
+ * pulsar_moe_route_ptrs + pulsar_moe_group_csr in one launch (no reference
+ * counterpart: the reference selects on the device, then builds pointers
+ * and the CSR on the host, crates/engine/src/lib.rs:7663-7670,
+ * 8255-8392). Outputs equal those three calls': selected / weights
+ * [n_tok][k_used], ptrs / slot_weights [n_tok][k_used + n_shared], gptrs,
+ * starts, pairs. k_used + n_shared <= 16, n_tok * (k_used + n_shared) <=
+ * 2048, k_used <= n_expert <= 1024; bank and shared are host pointers read
+ * at launch. */
+int pulsar_moe_route_group(void *selected, void *weights, void *ptrs, void *slot_weights,
+                           void *gptrs, void *starts, void *pairs, const void *logits,
+                           const void *router_bias, uint32_t n_expert, uint32_t k_used,
+                           float weight_scale, uint32_t softmax_mode,
+                           const pulsar_expert_bank *bank, const pulsar_expert_ptrs *shared,
+                           uint32_t n_shared, uint32_t n_tok, uint32_t max_groups);
+
+/* pulsar_moe_slot_sum + pulsar_moe_down_bias in one launch (no reference
+ * counterpart; the same sums in the same order, bit-identical to the two
+ * calls). */
+int pulsar_moe_slot_sum_bias(void *out, const void *partial, const void *ptrs,
+                             const void *weights, uint32_t out_dim, uint32_t n_used,
+                             uint32_t n_tok);
+
 /* Self-checks: small device runs of the entry points compared with host
  * mirrors (q8_K bit-exact; every stage of the MoE path for Q2_K, IQ2_XXS,
  * Q4_K, Q6_K and MXFP4; router modes 0, 1 and 2). They allocate and

@@ -34,6 +34,9 @@ SIGNATURES = {
     "pulsar_bw_read": [_vp, _u64, _vp],
     "pulsar_moe_route_ptrs": [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32],
     "pulsar_moe_group_csr": [_vp, _vp, _vp, _vp, _u32, _u32, _u32],
+    "pulsar_moe_route_group": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp,
+                               _u32, _u32, _u32],
+    "pulsar_moe_slot_sum_bias": [_vp, _vp, _vp, _vp, _u32, _u32, _u32],
     "pulsar_set_stream": [_vp],
     "pulsar_router_logits_q8": [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32],
     "pulsar_moe_pair_routed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp, _u32,

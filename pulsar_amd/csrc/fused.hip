@@ -62,25 +62,12 @@ template <uint32_t J>
 PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used,
                             float scale, uint32_t mode, const pulsar_expert_bank &bank, const SharedSlots &shared,
                             uint32_t slot) {
-    int32_t win[J];
-    float wprob[J];
-    float sum, wmax;
-    topk_wave<J>(lg, rbias, n_expert, k_used, mode, win, wprob, sum, wmax);
-    // k_used <= 64: winner k sits in lane k, slot 0
-    const uint32_t lane = threadIdx.x & 63u;
+    int32_t e;
     float wk;
-    if (mode == 1u) {
-        const float ek = lane < k_used ? expf(wprob[0] - wmax) : 0.0f;
-        float es = 0.0f;
-        for (uint32_t k = 0; k < k_used; k++)
-            es += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), (int)k));
-        wk = ek / es * scale;
-    } else {
-        wk = wprob[0] / fmaxf(sum, 6.103515625e-5f) * scale;
-    }
+    route_lane<J>(lg, rbias, n_expert, k_used, scale, mode, e, wk);
     SlotRoute r;
     if (slot < k_used) {
-        r.e = __builtin_amdgcn_readlane(win[0], (int)slot);
+        r.e = __builtin_amdgcn_readlane(e, (int)slot);
         r.w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), (int)slot));
         r.p = bank_ptrs(bank, n_expert, r.e);
     } else {

@@ -290,6 +290,29 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(float *__restrict__ out,
     out[gid] = acc;
 }
 
+// slot_sum_kernel then down_bias_kernel in one pass: the same two sums in
+// the same order, so the result is bit-identical to the two launches.
+__global__ __launch_bounds__(256) void slot_sum_bias_kernel(float *__restrict__ out,
+                                                            const float *__restrict__ partial,
+                                                            const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                            const float *__restrict__ weights,
+                                                            uint32_t out_dim, uint32_t n_used, uint64_t total) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const uint64_t token = gid / out_dim;
+    const uint64_t row = gid - token * out_dim;
+    float acc = 0.0f;
+    for (uint32_t s = 0; s < n_used; s++) acc += partial[(token * n_used + s) * out_dim + row];
+    float b = 0.0f;
+    for (uint32_t s = 0; s < n_used; s++) {
+        const uint64_t so = token * n_used + s;
+        const float *db = ptrs[so].down_b;
+        if (db) b += weights[so] * ldwf(db + row);
+    }
+    if (b != 0.0f) acc += b;
+    out[gid] = acc;
+}
+
 // out += sum_s w_s * down_b_s (pulsar_kernels.cu:3601-3619).
 __global__ __launch_bounds__(256) void down_bias_kernel(float *__restrict__ out,
                                                         const pulsar_expert_ptrs *__restrict__ ptrs,
@@ -540,4 +563,15 @@ extern "C" int pulsar_moe_down_bias(void *out, const void *ptrs, const void *wei
                        (float *)out, (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
                        out_dim, n_used, total);
     return launch_ok("moe down bias launch");
+}
+
+extern "C" int pulsar_moe_slot_sum_bias(void *out, const void *partial, const void *ptrs, const void *weights,
+                                        uint32_t out_dim, uint32_t n_used, uint32_t n_tok) {
+    if (!out || !partial || !ptrs || !weights || out_dim == 0 || n_used == 0 || n_tok == 0)
+        return reject("moe slot sum bias");
+    const uint64_t total = (uint64_t)n_tok * out_dim;
+    hipLaunchKernelGGL(slot_sum_bias_kernel, dim3((uint32_t)((total + 255u) / 256u)), dim3(256), 0, pk::stream(),
+                       (float *)out, (const float *)partial, (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
+                       out_dim, n_used, total);
+    return launch_ok("moe slot sum bias launch");
 }

@@ -115,6 +115,32 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
     }
 }
 
+// Routing of one token by the calling wave (modes 0 and 1, no sink
+// slots): lane k < k_used gets winner k (-1 if none) and its router weight,
+// normalised as router_select_kernel does (mode 1: softmax over the
+// winners with a sequential exp-sum; mode 0: probabilities over their
+// sequential sum, floored at 2^-14). k_used <= 64.
+template <uint32_t J>
+PK_DEV void route_lane(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used, float scale,
+                       uint32_t mode, int32_t &e, float &w) {
+    int32_t win[J];
+    float wprob[J];
+    float sum, wmax;
+    topk_wave<J>(lg, rbias, n_expert, k_used, mode, win, wprob, sum, wmax);
+    // winner k sits in lane k, slot 0
+    const uint32_t lane = threadIdx.x & 63u;
+    if (mode == 1u) {
+        const float ek = lane < k_used ? expf(wprob[0] - wmax) : 0.0f;
+        float es = 0.0f;
+        for (uint32_t k = 0; k < k_used; k++)
+            es += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), (int)k));
+        w = ek / es * scale;
+    } else {
+        w = wprob[0] / fmaxf(sum, 6.103515625e-5f) * scale;
+    }
+    e = win[0];
+}
+
 // f32 GEMV for router logits: one wave per (row, group of TG tokens);
 // lanes stride over K with 16-byte loads of the row and of the TG token
 // vectors, then a wave reduction per token; bias (if any) is added to the

@@ -70,11 +70,10 @@ PK_DEV uint32_t ptr_hash(uint64_t k) { return (uint32_t)(((k >> 4) * 0x9E3779B97
 // insert, atomic min of the pair index), group ids and group starts by
 // block scans, members scattered to their group's segment and put in pair
 // order by counting the smaller pair indices in the segment.
-__global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_ptrs *__restrict__ gptrs,
-                                                               uint32_t *__restrict__ starts,
-                                                               uint32_t *__restrict__ pairs,
-                                                               const pulsar_expert_ptrs *__restrict__ ptrs,
-                                                               uint32_t n, uint32_t n_used, uint32_t max_groups) {
+template <typename KeyFn, typename PtrFn>
+PK_DEV void csr_build(pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
+                      uint32_t *__restrict__ pairs, KeyFn key_of, PtrFn ptrs_of, uint32_t n, uint32_t n_used,
+                      uint32_t max_groups) {
     __shared__ unsigned long long tkey[kHashSlots];
     __shared__ uint32_t tfirst[kHashSlots];
     __shared__ uint32_t gid_of[kMaxCsrPairs];  // group id, at the index of the group's first pair
@@ -98,7 +97,7 @@ __global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_pt
 #pragma unroll
     for (uint32_t e = 0; e < 2; e++) {
         const uint32_t i = 2u * tid + e;
-        key[e] = i < n ? (uint64_t)(uintptr_t)ptrs[i].gate : 0ull;
+        key[e] = i < n ? key_of(i) : 0ull;
         if (key[e] != 0ull) {
             uint32_t h = ptr_hash(key[e]);
             for (;;) {  // the table has more free slots than pairs: ends
@@ -148,7 +147,7 @@ __global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_pt
         pairs[st + r] = ((i / n_used) << 4) | (i % n_used);
         if (isf[e] && g < max_groups) {
             starts[g] = st;
-            gptrs[g] = ptrs[i];
+            gptrs[g] = ptrs_of(i);
         }
     }
     // group slots past the last group: NULL with empty ranges. Groups past
@@ -159,6 +158,58 @@ __global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_pt
         starts[g] = end;
     }
     if (tid == 0) starts[max_groups] = end;
+}
+
+__global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_ptrs *__restrict__ gptrs,
+                                                               uint32_t *__restrict__ starts,
+                                                               uint32_t *__restrict__ pairs,
+                                                               const pulsar_expert_ptrs *__restrict__ ptrs,
+                                                               uint32_t n, uint32_t n_used, uint32_t max_groups) {
+    csr_build(
+            gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs[i].gate; },
+            [&](uint32_t i) { return ptrs[i]; }, n, n_used, max_groups);
+}
+
+// router_select (modes 0/1) + route_ptrs + group_csr in one block: the 16
+// waves route tokens (wave w takes tokens w, w + 16, ...; the arithmetic of
+// route_lane, as the fused pair kernel routes), keeping every pair's
+// expert in LDS, then the CSR is built from those as group_csr_kernel does.
+template <uint32_t J>
+__global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
+        int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
+        float *__restrict__ slot_w, pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
+        uint32_t *__restrict__ pairs, const float *__restrict__ logits, const float *__restrict__ rbias,
+        uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode, pulsar_expert_bank bank,
+        SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups) {
+    __shared__ int32_t eid_l[kMaxCsrPairs];  // routed expert, or -2 - s for shared slot s
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t n_slots = k_used + n_shared;
+    for (uint32_t t = wave; t < n_tok; t += kCsrThreads / 64u) {
+        int32_t e;
+        float w;
+        route_lane<J>(logits + (uint64_t)t * n_expert, rbias, n_expert, k_used, scale, mode, e, w);
+        if (lane < k_used) {
+            const uint64_t i = (uint64_t)t * n_slots + lane;
+            sel[(uint64_t)t * k_used + lane] = e;
+            rw[(uint64_t)t * k_used + lane] = w;
+            ptrs[i] = bank_ptrs(bank, n_expert, e);
+            slot_w[i] = w;
+            eid_l[i] = e < 0 ? -1 : e;
+        } else if (lane < n_slots) {
+            const uint64_t i = (uint64_t)t * n_slots + lane;
+            ptrs[i] = shared.p[lane - k_used];
+            slot_w[i] = 1.0f;
+            eid_l[i] = -2 - (int32_t)(lane - k_used);
+        }
+    }
+    __syncthreads();
+    auto ptrs_of = [&](uint32_t i) {
+        const int32_t e = eid_l[i];
+        return e >= -1 ? bank_ptrs(bank, n_expert, e) : shared.p[-2 - e];
+    };
+    csr_build(
+            gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs_of(i).gate; }, ptrs_of,
+            n_tok * n_slots, n_slots, max_groups);
 }
 
 }  // namespace pk
@@ -188,4 +239,33 @@ extern "C" int pulsar_moe_group_csr(void *gptrs, void *starts, void *pairs, cons
                        (uint32_t *)starts, (uint32_t *)pairs, (const pulsar_expert_ptrs *)ptrs,
                        n_tok * n_used, n_used, max_groups);
     return pk::launch_ok("moe group csr launch");
+}
+
+extern "C" int pulsar_moe_route_group(void *selected, void *weights, void *ptrs, void *slot_weights, void *gptrs,
+                                      void *starts, void *pairs, const void *logits, const void *router_bias,
+                                      uint32_t n_expert, uint32_t k_used, float weight_scale, uint32_t softmax_mode,
+                                      const pulsar_expert_bank *bank, const pulsar_expert_ptrs *shared,
+                                      uint32_t n_shared, uint32_t n_tok, uint32_t max_groups) {
+    const uint32_t n_slots = k_used + n_shared;
+    if (!selected || !weights || !ptrs || !slot_weights || !gptrs || !starts || !pairs || !logits || !bank ||
+        n_tok == 0 || k_used == 0 || k_used > n_expert || k_used > 64u || n_expert > 64u * pk::kMaxPerLane ||
+        softmax_mode > 1u || n_shared > pk::kMaxShared || (n_shared && !shared) || n_slots > 16u ||
+        max_groups == 0 || (uint64_t)n_tok * n_slots > pk::kMaxCsrPairs)
+        return pk::reject("moe route group");
+    pk::SharedSlots sh = {};
+    for (uint32_t s = 0; s < n_shared; s++) sh.p[s] = shared[s];
+#define PK_RG(J)                                                                                                 \
+    hipLaunchKernelGGL(pk::route_group_kernel<J>, dim3(1), dim3(pk::kCsrThreads), 0, pk::stream(),              \
+                       (int32_t *)selected, (float *)weights, (pulsar_expert_ptrs *)ptrs, (float *)slot_weights, \
+                       (pulsar_expert_ptrs *)gptrs, (uint32_t *)starts, (uint32_t *)pairs, (const float *)logits, \
+                       (const float *)router_bias, n_expert, k_used, weight_scale, softmax_mode, *bank, sh, n_shared, \
+                       n_tok, max_groups)
+    if (n_expert <= 256u)
+        PK_RG(4);
+    else if (n_expert <= 512u)
+        PK_RG(8);
+    else
+        PK_RG(16);
+#undef PK_RG
+    return pk::launch_ok("moe route group launch");
 }

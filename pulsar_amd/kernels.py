@@ -162,6 +162,23 @@ def moe_group_csr(gptrs, starts, pairs, ptrs, n_tok: int, n_used: int, max_group
     )
 
 
+def moe_slot_sum_bias(out, partial, ptrs, weights, out_dim: int, n_used: int, n_tok: int) -> None:
+    """moe_slot_sum + moe_down_bias in one launch (bit-identical)."""
+    _check(_lib.load().pulsar_moe_slot_sum_bias(_ptr(out), _ptr(partial), _ptr(ptrs), _ptr(weights), out_dim,
+                                                n_used, n_tok), "moe_slot_sum_bias")
+
+
+def moe_route_group(selected, weights, ptrs, slot_weights, gptrs, starts, pairs, logits, router_bias,
+                    n_expert: int, k_used: int, weight_scale: float, softmax_mode: int, bank: "ExpertBank", shared,
+                    n_tok: int, max_groups: int) -> None:
+    """router_select (modes 0/1) + moe_route_ptrs + moe_group_csr in one launch."""
+    arr, n_shared = _shared_array(shared)
+    _check(_lib.load().pulsar_moe_route_group(
+        _ptr(selected), _ptr(weights), _ptr(ptrs), _ptr(slot_weights), _ptr(gptrs), _ptr(starts), _ptr(pairs),
+        _ptr(logits), _ptr(router_bias), n_expert, k_used, weight_scale, softmax_mode, ctypes.byref(bank),
+        ctypes.cast(arr, ctypes.c_void_p), n_shared, n_tok, max_groups), "moe_route_group")
+
+
 def _shared_array(shared):
     shared = list(shared or [])
     arr = (_Ptrs6 * max(1, len(shared)))()

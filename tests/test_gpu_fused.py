@@ -104,3 +104,64 @@ def test_fused_error_contract(dev):
     with pytest.raises(K.KernelError):
         K.router_logits_q8(buf, buf, buf, buf, None, 0, 8, 1)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("E,k,n_tok,n_sh,mode,select_bias",
+                         [(128, 8, 16, 0, 1, False), (32, 4, 64, 0, 1, True), (256, 8, 3, 1, 1, False),
+                          (300, 6, 40, 2, 0, True), (12, 3, 200, 0, 1, False)])
+def test_route_group_matches_separate_calls(dev, E, k, n_tok, n_sh, mode, select_bias):
+    """router_select + moe_route_ptrs + moe_group_csr against the fused
+    launch: every output bit-identical (ties, an all-NaN token, shared
+    slots, a selection bias)."""
+    hidden = ffn = 256
+    L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=hidden, ffn=ffn, E=E + n_sh, n_used=k, n_tok=1)
+    bank = _bank(L)
+    shared = [L.dev_entries(E + i) for i in range(n_sh)]
+    n_slots = k + n_sh
+    f32 = dict(dtype=torch.float32, device=dev)
+    lg = rng.standard_normal((n_tok, E)).astype(np.float32)
+    lg[0, 1] = lg[0, 2]  # a tie: the lower index wins
+    if n_tok > 2:
+        lg[2] = np.nan  # routes nowhere (mode 1) / NaN scores (mode 0)
+    logits = torch.from_numpy(lg).to(dev)
+    sb = torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev) if select_bias else None
+    max_groups = min(E + n_sh, n_tok * n_slots)
+
+    def bufs():
+        return dict(sel=torch.zeros((n_tok, k), dtype=torch.int32, device=dev), rw=torch.zeros((n_tok, k), **f32),
+                    ptrs=torch.zeros(n_tok * n_slots * 48, dtype=torch.uint8, device=dev),
+                    slot_w=torch.zeros((n_tok, n_slots), **f32),
+                    gptrs=torch.zeros(max_groups * 48, dtype=torch.uint8, device=dev),
+                    starts=torch.zeros(max_groups + 1, dtype=torch.int32, device=dev),
+                    pairs=torch.zeros(n_tok * n_slots, dtype=torch.int32, device=dev))
+
+    a = bufs()
+    zero = torch.zeros(E, **f32)
+    K.router_select(a["sel"], a["rw"], logits, sb if sb is not None else zero, E, k, 1.25, n_tok, mode, 0)
+    K.moe_route_ptrs(a["ptrs"], a["slot_w"], a["sel"], a["rw"], bank, E, shared, n_tok, k)
+    K.moe_group_csr(a["gptrs"], a["starts"], a["pairs"], a["ptrs"], n_tok, n_slots, max_groups)
+    b = bufs()
+    K.moe_route_group(b["sel"], b["rw"], b["ptrs"], b["slot_w"], b["gptrs"], b["starts"], b["pairs"], logits, sb,
+                      E, k, 1.25, mode, bank, shared, n_tok, max_groups)
+    torch.cuda.synchronize()
+    for name in a:
+        ga, gb = down(a[name]), down(b[name])
+        assert np.array_equal(ga.view(np.uint8), gb.view(np.uint8)), name
+
+
+def test_slot_sum_bias_matches_separate_calls(dev):
+    L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=512, ffn=256, E=5, n_used=4, n_tok=7, biases=True,
+              null_slots=(2, 9))
+    hptrs, dptrs = L.ptrs()
+    f32 = dict(dtype=torch.float32, device=dev)
+    partial = torch.from_numpy(rng.standard_normal((L.n_tok * L.n_used, L.hidden)).astype(np.float32)).to(dev)
+    w = up_f32(L.w)
+    a = torch.zeros((L.n_tok, L.hidden), **f32)
+    K.moe_slot_sum(a, partial, L.hidden, L.n_used, L.n_tok)
+    K.moe_down_bias(a, dptrs, w, L.hidden, L.n_used, L.n_tok)
+    b = torch.zeros((L.n_tok, L.hidden), **f32)
+    K.moe_slot_sum_bias(b, partial, dptrs, w, L.hidden, L.n_used, L.n_tok)
+    torch.cuda.synchronize()
+    assert np.array_equal(down(a).view(np.uint32), down(b).view(np.uint32))
+    with pytest.raises(K.KernelError):
+        K.moe_route_group(a, a, a, a, a, a, a, a, None, 8, 17, 1.0, 1, _bank(L), None, 1, 8)  # > 16 slots
