@@ -131,7 +131,8 @@ def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
     ms = tm["ms"]
     alg = w.nbytes + xq.numel() + out.numel() * 4
     res = {
-        "kernel": "pk::mmq_kernel" if (n_tok >= 5 and quant == fm.QUANT_Q6_K) else "pk::matvec_kernel",
+        "kernel": ("pk::mmq_gemm_kernel" if (n_tok >= 5 and quant in (fm.QUANT_Q4_K, fm.QUANT_Q6_K))
+                   else "pk::matvec_kernel"),
         "alg_bytes": alg,
         "us_per_launch": ms * 1e3,
         "us_per_launch_eager": tm["ms_eager"] * 1e3,

@@ -16,8 +16,8 @@ namespace pk {
 
 // mmq.hip: MFMA kernel for token chunks; returns -1 when it has no kernel
 // for the format (the caller then uses the lane kernels)
-int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
-               uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes);
+int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
+                uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes);
 
 // Each wave streams row passes pass0, pass0 + n_waves, ...: the row's
 // weight units are requested first, then (once per wave) the token's
@@ -152,7 +152,7 @@ extern "C" int pulsar_matmul_kq(void *out, const void *w, const void *xq, uint32
     const uint8_t *wb = (const uint8_t *)w;
     const pulsar_block_q8_K *x = (const pulsar_block_q8_K *)xq;
     if (n_tok >= PK_MMQ_MIN_TOK) {
-        const int r = pk::launch_mmq(quant, o, wb, x, in_dim, out_dim, n_tok, row_bytes);
+        const int r = pk::launch_gemm(quant, o, wb, x, in_dim, out_dim, n_tok, row_bytes);
         if (r >= 0) return r;
     }
     switch (quant) {

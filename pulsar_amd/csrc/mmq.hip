@@ -1,8 +1,9 @@
 // mmq.hip - int8 matrix-core (v_mfma_i32_16x16x32_i8) kernels:
-//   mmq_kernel: the dense Q6_K matvec for token chunks (5..16 tokens per
-//     tile). A block computes 16 RT weight rows x 16 tokens; its NW waves
-//     split the row's super-blocks (split-K) and the partials are added in
-//     wave order through LDS (deterministic);
+//   mmq_gemm_kernel: the dense Q4_K / Q6_K matvec for token chunks and
+//     prefill (5 or more tokens; 16- or 32-token tiles). A block computes
+//     16 RT weight rows x 16 NT tokens; its waves split each K chunk's
+//     super-blocks and the partials are added in wave order through LDS
+//     (deterministic);
 //   moe_grouped_mmq_kq_kernel: the grouped MoE stages (16 rows x up to 16
 //     (token, slot) pairs of one expert per MFMA tile) for Q2_K, IQ2_XXS and
 //     MXFP4 experts.
@@ -82,169 +83,305 @@ struct MmaQ6K {
     }
 };
 
-#ifndef PK_MMQ_RT
-#define PK_MMQ_RT 2u
-#endif
-#ifndef PK_MMQ_C
-#define PK_MMQ_C 4u
-#endif
-
-// Tile of 16 RT rows x 16 tokens, K walked in chunks of C super-blocks.
-// Each chunk's weights (16 RT rows x C super-blocks) and activations (16
-// tokens x C super-blocks) are copied HBM -> LDS with row-contiguous
-// 16-byte loads (a wave's load covers 4 consecutive super-blocks of one
-// row), the next chunk's loads are issued before the current chunk's MFMAs,
-// and wave (rt, sb) = (w / C, w % C) takes row tile rt, super-block sb of
-// each chunk. LDS rows are padded so the 16 rows (tokens) an MFMA operand
-// read touches fall in distinct banks.
-template <uint32_t Q, uint32_t RT, uint32_t C>
-struct MmqTile {
-    static constexpr uint32_t NW = RT * C;                          // waves
-    static constexpr uint32_t NT = 64u * NW;                        // threads
-    static constexpr uint32_t kRows = 16u * RT;
-    static constexpr uint32_t kSb = MmaQ6K::kSbBytes;               // bytes per row super-block
-    static constexpr uint32_t kChunks = (kSb + 15u) / 16u;          // 16-byte loads per row super-block
-    static constexpr uint32_t kSlot = 16u * kChunks;                // LDS bytes per row super-block
-    // the last load of a super-block reads its final 16 bytes (kSb - 16 ..)
-    // and is stored at slot offset 16 (kChunks - 1): d lands here
-    static constexpr uint32_t kDSlot = 16u * (kChunks - 1u) + MmaQ6K::kDOff - (kSb - 16u);
-    static constexpr uint32_t kRowPitch = C * kSlot + 16u;          // LDS bytes per row (padded)
-    static constexpr uint32_t kActPitch = 256u + 16u;               // LDS bytes per (token, super-block)
-    static constexpr uint32_t kWLoads = kRows * C * 16u / NT;       // weight loads per thread
-    static constexpr uint32_t kALoads = 16u * C * 16u / NT;         // activation loads per thread
-    static_assert(kRows * C * 16u % NT == 0 && 16u * C * 16u % NT == 0, "tile shape");
-    static_assert(C * 16u <= NT, "one activation scale per thread");
+// --------------------------------------------- dense GEMM (chunks, prefill) --
+// Q4_K for the MFMA kernels: K slice t (32 values) is sub-block t; lane
+// group kq holds qs bytes 32 (t / 2) + 8 kq + [0, 8), nibble t % 2. Codes
+// 0..15 are int8 as they are; the 6-bit scale multiplies each slice's D
+// (24-bit products), and the min term sum_t m_t (bsums[2t] + bsums[2t+1])
+// comes from two MFMAs on those sums split as 128 h + l (l in [0, 128),
+// |h| <= 32). Super-block value xd yd isum - xmin yd msum (cpu_dot.rs:250-279).
+struct MmaQ4K {
+    static constexpr uint32_t kSbBytes = 144;
+    struct W {
+        uint2 q[4];  // qs bytes 32c + 8kq + [0, 8)
+        uint4 hdr;   // d, dmin, scales[12]
+    };
+    PK_DEV static W load_lds(const uint8_t *blk, uint32_t kq) {
+        W w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.q[c] = lds64(blk + 16u + 32u * c + 8u * kq);
+        w.hdr = lds128(blk);
+        return w;
+    }
+    PK_DEV static uint2 codes(const W &w, int t) {
+        const uint2 q = w.q[t >> 1];
+        const uint32_t sh = 4u * (t & 1);
+        return make_uint2((q.x >> sh) & 0x0f0f0f0fu, (q.y >> sh) & 0x0f0f0f0fu);
+    }
 };
 
-template <uint32_t Q, uint32_t RT, uint32_t C>
-__global__ __launch_bounds__(64 * RT * C) void mmq_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
-                                                          const pulsar_block_q8_K *__restrict__ xq, uint32_t nb,
-                                                          uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
-    using T = MmqTile<Q, RT, C>;
-    __shared__ __align__(16) uint8_t wl[T::kRows * T::kRowPitch];
-    __shared__ __align__(16) uint8_t al[C * 16u * T::kActPitch];
-    __shared__ __align__(16) float yl[C * 16u];
-    __shared__ float part[T::NW][16][17];
+// Per-format pieces of the dense GEMM: super-block bytes, 16-byte copies
+// per row super-block (the last one may overlap the previous: it ends at
+// the super-block's end), the LDS slot offset of f16 d, bsums needed.
+template <uint32_t Q>
+struct GemmFmt;
+template <>
+struct GemmFmt<PULSAR_QUANT_Q6_K> {
+    static constexpr uint32_t kSb = 210, kChunks = 14, kDSlot = 16u * 13u + 208u - 194u;
+    static constexpr bool kBsums = false;
+};
+template <>
+struct GemmFmt<PULSAR_QUANT_Q4_K> {
+    static constexpr uint32_t kSb = 144, kChunks = 9, kDSlot = 0;
+    static constexpr bool kBsums = true;
+};
+
+// bsums b[2t] + b[2t + 1] for t = 4 (kq & 1) + [0, 4) of a token, split as
+// 128 h + l: l bytes (kq < 2) or h bytes (kq >= 2)
+PK_DEV uint32_t pair_sum_bytes(uint4 b, bool high) {
+    const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+    uint32_t out = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int32_t s = (int32_t)(int16_t)(w[j] & 0xffffu) + (int32_t)(int16_t)(w[j] >> 16);
+        const uint32_t v = high ? (uint32_t)(s >> 7) & 0xffu : (uint32_t)s & 0x7fu;
+        out |= v << (8 * j);
+    }
+    return out;
+}
+
+// Block = 16 RT rows x 16 NT tokens, K in chunks of C super-blocks, NW =
+// RT C waves. Per chunk the rows' super-blocks (row-contiguous 16-byte
+// copies) and the tokens' q8 values (+ bsums for Q4_K, + d) are staged in
+// LDS; wave (rt, sb) decodes row tile rt, super-block sb of the chunk once
+// and multiplies it with all NT token tiles. The next chunk's loads are
+// issued before the current chunk is decoded; every thread issues every
+// load (clamped, stored or not), so the waits count exactly one chunk.
+// The C partials of a row tile are added in wave order (deterministic).
+template <uint32_t Q, uint32_t RT, uint32_t C, uint32_t NT>
+__global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
+                                                               const pulsar_block_q8_K *__restrict__ xq, uint32_t nb,
+                                                               uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
+    using F = GemmFmt<Q>;
+    constexpr uint32_t NW = RT * C, NTH = 64u * NW, TOK = 16u * NT, ROWS = 16u * RT;
+    constexpr uint32_t kSlot = 16u * F::kChunks;
+    constexpr uint32_t kRowPitch = C * kSlot + 16u;  // LDS bytes per row
+    constexpr uint32_t kActPitch = 272u;             // LDS bytes per (super-block, token) q8 values
+    constexpr uint32_t kAPer = F::kBsums ? 18u : 16u;  // 16-byte pieces per (token, super-block)
+    constexpr uint32_t kWP = ROWS * C * F::kChunks, kWL = (kWP + NTH - 1u) / NTH;
+    constexpr uint32_t kAP = TOK * C * kAPer, kAL = (kAP + NTH - 1u) / NTH;
+    constexpr uint32_t kYL = (TOK * C + NTH - 1u) / NTH;
+    constexpr uint32_t kWlBytes = ROWS * kRowPitch, kAlBytes = C * TOK * kActPitch;
+    constexpr uint32_t kBlBytes = F::kBsums ? C * TOK * 32u : 0u;
+    static_assert(NW * 16u * (TOK + 1u) * 4u <= kAlBytes, "partials alias the activation area");
+    __shared__ __align__(16) uint8_t lds[kWlBytes + kAlBytes + kBlBytes + C * TOK * 4u];
+    uint8_t *wl = lds, *al = lds + kWlBytes, *bl = al + kAlBytes;
+    float *yl = (float *)(bl + kBlBytes);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
-    const uint32_t r0 = blockIdx.x * T::kRows, t0 = blockIdx.y * 16u;
+    const uint32_t t0 = blockIdx.x * TOK, r0 = blockIdx.y * ROWS;
     const uint8_t *xb = (const uint8_t *)xq;
     const uint64_t tok_bytes = (uint64_t)nb * 292u;
-
-    // ---- HBM -> registers -> LDS copy of one chunk (super-blocks kb ..).
-    // Per-thread source pointers (chunk 0) and LDS offsets are fixed.
-    const uint8_t *wsrc[T::kWLoads];
-    uint32_t wsb[T::kWLoads], wdst[T::kWLoads];
-    bool wact[T::kWLoads];
+    const uint8_t *wsrc[kWL];
+    uint32_t wsb[kWL], wdst[kWL];
 #pragma unroll
-    for (uint32_t m = 0; m < T::kWLoads; m++) {
-        const uint32_t f = tid + T::NT * m, c = f & 15u, rs = f >> 4;
-        const uint32_t row = rs / C, sb = rs % C;
+    for (uint32_t m = 0; m < kWL; m++) {
+        const uint32_t f = tid + NTH * m, ff = f < kWP ? f : kWP - 1u;
+        const uint32_t c = ff % F::kChunks, rs = ff / F::kChunks, row = rs / C, sb = rs % C;
         const uint32_t gr = r0 + row < out_dim ? r0 + row : out_dim - 1u;
-        const uint32_t off = 16u * c < T::kSb - 16u ? 16u * c : T::kSb - 16u;
-        wsrc[m] = w + (uint64_t)gr * row_bytes + (uint64_t)sb * T::kSb + off;
+        wsrc[m] = w + (uint64_t)gr * row_bytes + (16u * c < F::kSb - 16u ? 16u * c : F::kSb - 16u);
         wsb[m] = sb;
-        wdst[m] = row * T::kRowPitch + sb * T::kSlot + 16u * c;
-        wact[m] = c < T::kChunks;
+        wdst[m] = f < kWP ? row * kRowPitch + sb * kSlot + 16u * c : UINT32_MAX;
     }
-    const uint8_t *asrc[T::kALoads];
-    uint32_t asb[T::kALoads], adst[T::kALoads];
+    const uint8_t *asrc[kAL];
+    uint32_t asb[kAL], adst[kAL];
 #pragma unroll
-    for (uint32_t m = 0; m < T::kALoads; m++) {
-        const uint32_t f = tid + T::NT * m, c = f & 15u, ts = f >> 4;
-        const uint32_t t = ts / C, sb = ts % C;
+    for (uint32_t m = 0; m < kAL; m++) {
+        const uint32_t f = tid + NTH * m, ff = f < kAP ? f : kAP - 1u;
+        const uint32_t c = ff % kAPer, ts = ff / kAPer, t = ts / C, sb = ts % C;
         const uint32_t gt = t0 + t < n_tok ? t0 + t : n_tok - 1u;
-        asrc[m] = xb + gt * tok_bytes + (uint64_t)sb * 292u + 4u + 16u * c;
+        asrc[m] = xb + gt * tok_bytes + (c < 16u ? 4u + 16u * c : 260u + 16u * (c - 16u));
         asb[m] = sb;
-        adst[m] = (sb * 16u + t) * T::kActPitch + 16u * c;
+        adst[m] = f >= kAP ? UINT32_MAX
+                  : c < 16u ? kWlBytes + (sb * TOK + t) * kActPitch + 16u * c
+                            : kWlBytes + kAlBytes + (sb * TOK + t) * 32u + 16u * (c - 16u);
     }
-    const uint32_t ysb = tid % C, yt = tid / C;
-    const uint8_t *ysrc = xb + (t0 + yt < n_tok ? t0 + yt : n_tok - 1u) * tok_bytes + (uint64_t)ysb * 292u;
-    const bool yact = tid < C * 16u;
-
-    uint4 wreg[T::kWLoads], areg[T::kALoads];
-    uint32_t yreg = 0;
+    const uint8_t *ysrc[kYL];
+    uint32_t ysb[kYL], ydst[kYL];
+#pragma unroll
+    for (uint32_t m = 0; m < kYL; m++) {
+        const uint32_t f = tid + NTH * m, ff = f < TOK * C ? f : TOK * C - 1u;
+        const uint32_t t = ff / C, sb = ff % C;
+        ysrc[m] = xb + (t0 + t < n_tok ? t0 + t : n_tok - 1u) * tok_bytes;
+        ysb[m] = sb;
+        ydst[m] = f < TOK * C ? sb * TOK + t : UINT32_MAX;
+    }
+    uint4 wreg[kWL], areg[kAL];
+    uint32_t yreg[kYL];
     auto gload = [&](uint32_t kb) {
 #pragma unroll
-        for (uint32_t m = 0; m < T::kWLoads; m++)
-            if (wact[m] && kb + wsb[m] < nb) wreg[m] = ld128(wsrc[m] + (uint64_t)kb * T::kSb);
+        for (uint32_t m = 0; m < kWL; m++)
+            wreg[m] = ldw128(wsrc[m] + (uint64_t)(kb + wsb[m] < nb ? kb + wsb[m] : nb - 1u) * F::kSb);
 #pragma unroll
-        for (uint32_t m = 0; m < T::kALoads; m++)
-            if (kb + asb[m] < nb) areg[m] = ld128(asrc[m] + (uint64_t)kb * 292u);
-        if (yact && kb + ysb < nb) yreg = ld32(ysrc + (uint64_t)kb * 292u);
+        for (uint32_t m = 0; m < kAL; m++)
+            areg[m] = ld128(asrc[m] + (uint64_t)(kb + asb[m] < nb ? kb + asb[m] : nb - 1u) * 292u);
+#pragma unroll
+        for (uint32_t m = 0; m < kYL; m++)
+            yreg[m] = ld32(ysrc[m] + (uint64_t)(kb + ysb[m] < nb ? kb + ysb[m] : nb - 1u) * 292u);
     };
     auto lstore = [&]() {
 #pragma unroll
-        for (uint32_t m = 0; m < T::kWLoads; m++)
-            if (wact[m]) *(uint4 *)(wl + wdst[m]) = wreg[m];
+        for (uint32_t m = 0; m < kWL; m++)
+            if ((m + 1u) * NTH <= kWP || wdst[m] != UINT32_MAX) *(uint4 *)(wl + wdst[m]) = wreg[m];
 #pragma unroll
-        for (uint32_t m = 0; m < T::kALoads; m++) *(uint4 *)(al + adst[m]) = areg[m];
-        if (yact) yl[ysb * 16u + yt] = __builtin_bit_cast(float, yreg);
+        for (uint32_t m = 0; m < kAL; m++)
+            if ((m + 1u) * NTH <= kAP || adst[m] != UINT32_MAX) *(uint4 *)(lds + adst[m]) = areg[m];
+#pragma unroll
+        for (uint32_t m = 0; m < kYL; m++)
+            if ((m + 1u) * NTH <= TOK * C || ydst[m] != UINT32_MAX) yl[ydst[m]] = __builtin_bit_cast(float, yreg[m]);
     };
 
     const uint32_t rt = wave / C, sbw = wave % C;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float acc[NT][4];
+#pragma unroll
+    for (uint32_t n = 0; n < NT; n++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[n][r] = 0.0f;
+    auto chunk = [&](uint32_t kb) {
+        if (kb + sbw < nb) {
+            const uint8_t *wrow = wl + (rt * 16u + i) * kRowPitch + sbw * kSlot;
+            const uint8_t *abase = al + (sbw * TOK + i) * kActPitch + 8u * kq;
+            if constexpr (Q == PULSAR_QUANT_Q6_K) {
+                const MmaQ6K::W wv = MmaQ6K::load_lds(wrow, kq, F::kDSlot);
+                int32_t isum[NT][4];
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) isum[n][r] = 0;
+#pragma unroll
+                for (int st = 0; st < 8; st++) {
+                    const int h = st >> 2, q = st & 3;
+                    const uint2 c = MmaQ6K::codes(wv, h, q);
+                    const uint2 c_lo = kq < 2 ? c : make_uint2(0u, 0u);
+                    const int32_t s0 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q);
+                    const int32_t s1 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q + 1);
+#pragma unroll
+                    for (uint32_t n = 0; n < NT; n++) {
+                        const uint2 a = lds64(abase + 16u * n * kActPitch + 32u * st);
+                        const v4i d_all = mfma16x16x32(a, c);
+                        const v4i d_lo = mfma16x16x32(a, c_lo);
+                        // |d| < 2^17, |s| < 2^8: 24-bit multiplies are exact
+#pragma unroll
+                        for (int r = 0; r < 4; r++) isum[n][r] += __mul24(s0 - s1, d_lo[r]) + __mul24(s1, d_all[r]);
+                    }
+                }
+                const float xd = f16f((uint16_t)wv.d);
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++) {
+                    const float4 yd4 = lds_f4(yl + sbw * TOK + 16u * n + 4u * kq);
+                    const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[n][r] += xd * yd[r] * (float)isum[n][r];
+                }
+            } else {
+                const MmaQ4K::W wv = MmaQ4K::load_lds(wrow, kq);
+                int32_t isum[NT][4];
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) isum[n][r] = 0;
+                uint32_t mins[2] = {0u, 0u};
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    int32_t sc, mn;
+                    Fmt<PULSAR_QUANT_Q4_K>::scale_min(wv.hdr, (uint32_t)t, sc, mn);
+                    mins[t >> 2] |= (uint32_t)mn << (8 * (t & 3));
+                    const uint2 b = MmaQ4K::codes(wv, t);
+#pragma unroll
+                    for (uint32_t n = 0; n < NT; n++) {
+                        const v4i d = mfma16x16x32(lds64(abase + 16u * n * kActPitch + 32u * t), b);
+                        // |d| < 2^17, sc < 64
+#pragma unroll
+                        for (int r = 0; r < 4; r++) isum[n][r] += __mul24(sc, d[r]);
+                    }
+                }
+                // min term: K slots [l_0..3 | l_4..7 | h_0..3 | h_4..7] per lane group
+                // against the mins in lane groups 0, 1 (D_l) and 2, 3 (D_h)
+                const uint32_t mw = mins[kq & 1u];
+                const uint2 bl_ = kq < 2u ? make_uint2(mw, 0u) : make_uint2(0u, 0u);
+                const uint2 bh_ = kq < 2u ? make_uint2(0u, 0u) : make_uint2(mw, 0u);
+                const uint32_t xh = wv.hdr.x;
+                const float xd = f16f((uint16_t)xh), xmin = f16f((uint16_t)(xh >> 16));
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++) {
+                    const uint4 bs = lds128(bl + (sbw * TOK + 16u * n + i) * 32u + 16u * (kq & 1u));
+                    const uint2 alh = make_uint2(pair_sum_bytes(bs, kq >= 2u), 0u);
+                    const v4i dl = mfma16x16x32(alh, bl_);
+                    const v4i dh = mfma16x16x32(alh, bh_);
+                    const float4 yd4 = lds_f4(yl + sbw * TOK + 16u * n + 4u * kq);
+                    const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int32_t msum = dl[r] + 128 * dh[r];
+                        acc[n][r] += xd * yd[r] * (float)isum[n][r] - xmin * yd[r] * (float)msum;
+                    }
+                }
+            }
+        }
+    };
     gload(0);
-    for (uint32_t kb = 0; kb < nb; kb += C) {
+    uint32_t kb = 0;
+    for (; kb + C < nb; kb += C) {
         lstore();
         __syncthreads();
-        if (kb + C < nb) gload(kb + C);  // in flight during this chunk's MFMAs
-        if (kb + sbw < nb) {
-            uint2 a[8];
-            const uint8_t *ab = al + (sbw * 16u + i) * T::kActPitch + 8u * kq;
-#pragma unroll
-            for (int st = 0; st < 8; st++) a[st] = lds64(ab + 32u * st);
-            const float4 yd4 = lds_f4(yl + sbw * 16u + 4u * kq);
-            const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
-            const MmaQ6K::W wv =
-                MmaQ6K::load_lds(wl + (rt * 16u + i) * T::kRowPitch + sbw * T::kSlot, kq, T::kDSlot);
-            int32_t isum[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int st = 0; st < 8; st++) {
-                const int h = st >> 2, q = st & 3;
-                const uint2 c = MmaQ6K::codes(wv, h, q);
-                const uint2 c_lo = kq < 2 ? c : make_uint2(0u, 0u);
-                const v4i d_all = mfma16x16x32(a[st], c);
-                const v4i d_lo = mfma16x16x32(a[st], c_lo);
-                const int32_t s0 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q);
-                const int32_t s1 = (int32_t)(int8_t)byte_of(wv.sc, 8 * h + 2 * q + 1);
-#pragma unroll
-                // |d| < 2^17, |s| < 2^8: 24-bit multiplies are exact
-                for (int r = 0; r < 4; r++) isum[r] += __mul24(s0 - s1, d_lo[r]) + __mul24(s1, d_all[r]);
-            }
-            const float xd = f16f((uint16_t)wv.d);
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] += xd * yd[r] * (float)isum[r];
-        }
+        gload(kb + C);  // in flight while this chunk is decoded
+        chunk(kb);
         __syncthreads();
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) part[wave][i][4 * kq + r] = acc[r];
+    lstore();  // the last chunk: nothing left to prefetch
     __syncthreads();
-    for (uint32_t e = tid; e < 16u * T::kRows; e += T::NT) {
-        const uint32_t row = e % T::kRows, tok = e / T::kRows;
+    chunk(kb);
+    __syncthreads();
+    // partials [wave][row][token] over the activation area (all reads of it are done)
+    float *part = (float *)al;
+#pragma unroll
+    for (uint32_t n = 0; n < NT; n++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) part[(wave * 16u + i) * (TOK + 1u) + 16u * n + 4u * kq + r] = acc[n][r];
+    __syncthreads();
+    for (uint32_t e = tid; e < TOK * ROWS; e += NTH) {
+        const uint32_t row = e % ROWS, tok = e / ROWS;
         if (r0 + row < out_dim && t0 + tok < n_tok) {
             const uint32_t prt = row / 16u;
-            float v = part[prt * C][row % 16u][tok];
+            float v = part[((prt * C) * 16u + row % 16u) * (TOK + 1u) + tok];
 #pragma unroll
-            for (uint32_t k = 1; k < C; k++) v += part[prt * C + k][row % 16u][tok];
+            for (uint32_t k = 1; k < C; k++) v += part[((prt * C + k) * 16u + row % 16u) * (TOK + 1u) + tok];
             out[(uint64_t)(t0 + tok) * out_dim + r0 + row] = v;
         }
     }
 }
 
-int launch_mmq(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
-               uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
-    constexpr uint32_t RT = PK_MMQ_RT, C = PK_MMQ_C;
+// token-tile width by chunk size: 32-token tiles (measured on Q4_K / Q6_K
+// 4096-wide rows at 64 and 256 tokens) beat 16-token tiles, which decode
+// every weight twice as often, and 64-token tiles, which leave too few blocks
+#ifndef PK_GEMM_NT2
+#define PK_GEMM_NT2 32u
+#endif
+
+template <uint32_t Q>
+static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t nb, uint32_t out_dim,
+                         uint32_t n_tok, uint64_t row_bytes) {
+#define PK_GEMM(RT, C, NT)                                                                                   \
+    hipLaunchKernelGGL((mmq_gemm_kernel<Q, RT, C, NT>), dim3((n_tok + 16u * NT - 1u) / (16u * NT),            \
+                                                             (out_dim + 16u * RT - 1u) / (16u * RT)),          \
+                       dim3(64 * RT * C), 0, pk::stream(), out, w, xq, nb, out_dim, n_tok, row_bytes)
+    if (n_tok >= PK_GEMM_NT2)
+        PK_GEMM(2, 2, 2);
+    else
+        PK_GEMM(2, 4, 1);
+#undef PK_GEMM
+    return launch_ok("matmul_kq gemm launch");
+}
+
+// MFMA GEMM for token chunks / prefill (Q4_K, Q6_K); -1 for other formats.
+int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
+                uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
     const uint32_t nb = in_dim / 256u;
-    const dim3 grid((out_dim + 16u * RT - 1u) / (16u * RT), (n_tok + 15u) / 16u);
+    if ((uint64_t)((out_dim + 31u) / 32u) > 65535u) return -1;  // grid y
     switch (quant) {
-    case PULSAR_QUANT_Q6_K:
-        hipLaunchKernelGGL((mmq_kernel<PULSAR_QUANT_Q6_K, RT, C>), grid, dim3(64 * RT * C), 0, pk::stream(), out,
-                           w, xq, nb, out_dim, n_tok, row_bytes);
-        return launch_ok("matmul_kq mmq launch");
-    default:
-        return -1;  // no MFMA kernel for this format: caller falls back
+    case PULSAR_QUANT_Q6_K: return launch_gemm_q<PULSAR_QUANT_Q6_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
+    case PULSAR_QUANT_Q4_K: return launch_gemm_q<PULSAR_QUANT_Q4_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
+    default: return -1;
     }
 }
 

@@ -75,7 +75,8 @@ def unit_scale_matrix(quant, rows, n, seed):
 
 @pytest.mark.parametrize("quant", DENSE)
 @pytest.mark.parametrize("n,rows,n_tok", [(256, 37, 1), (2048, 64, 1), (4096, 33, 3), (12288, 9, 1),
-                                          (256, 21, 7), (4096, 37, 16), (2048, 50, 20), (1024, 16, 5)])
+                                          (256, 21, 7), (4096, 37, 16), (2048, 50, 20), (1024, 16, 5),
+                                          (1024, 50, 64), (512, 33, 100), (768, 70, 40)])
 def test_matvec_integer_stage_exact(dev, quant, n, rows, n_tok):
     w = unit_scale_matrix(quant, rows, n, n + rows)
     xq = unit_scale_xq(n_tok, n)
@@ -91,7 +92,7 @@ def test_matvec_integer_stage_exact(dev, quant, n, rows, n_tok):
 @pytest.mark.parametrize("quant", DENSE)
 @pytest.mark.parametrize("n,rows,n_tok", [(256, 5, 1), (2048, 130, 1), (4096, 77, 2), (4096, 40, 5),
                                           (4096, 24, 16), (8192, 19, 1), (20480, 7, 1),
-                                          (2816, 33, 9), (4096, 70, 33)])
+                                          (2816, 33, 9), (4096, 70, 33), (2048, 36, 70)])
 def test_matvec_fp32_parity(dev, quant, n, rows, n_tok):
     w = synth.quant_matrix(quant, rows, n, synth.rng_for(n * rows + n_tok, "mv"))
     x = rng.standard_normal((n_tok, n)).astype(np.float32)
@@ -105,11 +106,11 @@ def test_matvec_fp32_parity(dev, quant, n, rows, n_tok):
         assert_rows_close(got[t], np.array(vals, np.float32), np.array(scale), f"q{quant} n{n} t{t}")
 
 
-@pytest.mark.parametrize("n_tok", [1, 16])
-def test_matvec_padded_row_stride(dev, n_tok):
+@pytest.mark.parametrize("quant,n_tok", [(QUANT_Q6_K, 1), (QUANT_Q6_K, 16), (QUANT_Q4_K, 16), (QUANT_Q4_K, 64)])
+def test_matvec_padded_row_stride(dev, quant, n_tok):
     # row_bytes larger than the packed row: rows start row_bytes apart
-    # (n_tok 16 runs the MFMA kernel)
-    n, rows, quant = 1024, 21, QUANT_Q6_K
+    # (n_tok >= 5 runs the MFMA kernels)
+    n, rows = 1024, 21
     rb = row_bytes(quant, n)
     w = synth.quant_matrix(quant, rows, n, synth.rng_for(5, "pad"))
     padded = np.zeros((rows, rb + 46), np.uint8)
