@@ -451,6 +451,26 @@ struct GmmqFmt<PULSAR_QUANT_MXFP4> {
         return 17u * (b < lim ? b : lim - 1u);
     }
 };
+template <>
+struct GmmqFmt<PULSAR_QUANT_Q4_K> {
+    static constexpr uint32_t kPieces = 9, kTails = 0, kTailBytes = 4;  // the whole 144 bytes
+    static constexpr uint32_t kTailSlot = 0;
+    static constexpr uint32_t kSlot = 144;
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        return (sb < lim ? sb : lim - 1u) * 144u + 16u * c;
+    }
+    PK_DEV static uint32_t tail_off(uint32_t, uint32_t, uint32_t) { return 0u; }
+};
+template <>
+struct GmmqFmt<PULSAR_QUANT_Q6_K> {
+    static constexpr uint32_t kPieces = 13, kTails = 1, kTailBytes = 2;  // bytes 0..207, then d
+    static constexpr uint32_t kTailSlot = 208;
+    static constexpr uint32_t kSlot = 224;
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        return (sb < lim ? sb : lim - 1u) * 210u + 16u * c;
+    }
+    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t, uint32_t lim) { return (sb < lim ? sb : lim - 1u) * 210u + 208u; }
+};
 #ifndef PK_GQ_SBS
 #define PK_GQ_SBS 2u
 #endif
@@ -494,12 +514,14 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     constexpr uint32_t NM = PAIR ? 2 : 1;
     constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
     constexpr bool kMx = Q == PULSAR_QUANT_MXFP4;
-    constexpr uint32_t S = kMx ? 1u : kGqSbs;  // an MXFP4 super-block row is 136 contiguous bytes already
+    // MXFP4, Q4_K and Q6_K super-block rows are 136-210 contiguous bytes already
+    constexpr uint32_t S = (kMx || Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q6_K) ? 1u : kGqSbs;
     constexpr uint32_t kRowL = S * F::kSlot + 16u;        // LDS bytes per row (S slots, padded)
     constexpr uint32_t kWp = NM * 16u * S * F::kPieces;  // weight pieces per step
     constexpr uint32_t kWj = (kWp + 63u) / 64u;         // ... per lane
     constexpr uint32_t kTp = NM * 16u * S * F::kTails;  // tails per step
     constexpr uint32_t kTj = (kTp + 63u) / 64u;
+    constexpr uint32_t kTjA = kTj > 0u ? kTj : 1u;  // array extent
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint2 lut[kIq2 ? kIq2LutRows : 1];
     __shared__ __align__(16) uint8_t wl[4][NM * 16u * kRowL];  // [wave][matrix][row][step slot]
@@ -540,12 +562,13 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
         wdst[j] = q < kWp ? (rm * kRowL + sl * F::kSlot + 16u * c) : UINT32_MAX;
     }
     // tails (d / dmin, MXFP4 e): kTails per (matrix, row, super-block of the step)
-    const uint8_t *tsrc[kTj];
-    uint32_t tsc[kTj], tdst[kTj];
+    const uint8_t *tsrc[kTjA];
+    uint32_t tsc[kTjA], tdst[kTjA];
 #pragma unroll
     for (uint32_t j = 0; j < kTj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
-        const uint32_t c = qq % F::kTails, rs = qq / F::kTails, sl = rs % S, rm = rs / S;
+        const uint32_t c = qq % (F::kTails ? F::kTails : 1u), rs = qq / (F::kTails ? F::kTails : 1u);
+        const uint32_t sl = rs % S, rm = rs / S;
         tsrc[j] = row_src(rm / 16u, rm % 16u);
         tsc[j] = sl << 8 | c;
         tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot + c) : UINT32_MAX;
@@ -564,7 +587,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
         __syncthreads();
         if (!active) continue;  // wave-uniform; the block's barriers above are reached
         uint4 wv[kWj];
-        uint32_t tv[kTj];
+        uint32_t tv[kTjA];
         auto issue = [&](uint32_t step) {
 #pragma unroll
             for (uint32_t j = 0; j < kWj; j++)
@@ -572,7 +595,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
 #pragma unroll
             for (uint32_t j = 0; j < kTj; j++) {
                 const uint8_t *tp = tsrc[j] + F::tail_off(step * S + (tsc[j] >> 8), tsc[j] & 0xffu, lim);
-                tv[j] = F::kTailBytes == 4u ? ldw32(tp) : ldw8(tp);
+                tv[j] = F::kTailBytes == 4u ? ldw32(tp) : F::kTailBytes == 2u ? (uint32_t)ldw16(tp) : ldw8(tp);
             }
         };
         // lane (pair i, kq): its pair's record (the last pair's past the tile)
@@ -627,6 +650,78 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                 for (uint32_t mt = 0; mt < NM; mt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[mt][r] += yd[r] * f[mt][r];
+            } else if constexpr (Q == PULSAR_QUANT_Q6_K) {
+                // two MFMAs per 32-value step (both 16-value scale groups, then
+                // the first alone): sc0 D0 + sc1 D1 = (sc0 - sc1) D_lo + sc1 D_all
+                MmaQ6K::W wv[NM];
+                int32_t isum[NM][4];
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    wv[mt] = MmaQ6K::load_lds(ws + mt * 16u * kRowL, kq, F::kTailSlot);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) isum[mt][r] = 0;
+                }
+#pragma unroll
+                for (int st = 0; st < 8; st++) {
+                    const int h = st >> 2, q = st & 3;
+                    const uint2 a = a_at((uint32_t)st);
+#pragma unroll
+                    for (uint32_t mt = 0; mt < NM; mt++) {
+                        const uint2 c = MmaQ6K::codes(wv[mt], h, q);
+                        const v4i d_all = mfma16x16x32(a, c);
+                        const v4i d_lo = mfma16x16x32(a, kq < 2 ? c : make_uint2(0u, 0u));
+                        const int32_t s0 = (int32_t)(int8_t)byte_of(wv[mt].sc, 8 * h + 2 * q);
+                        const int32_t s1 = (int32_t)(int8_t)byte_of(wv[mt].sc, 8 * h + 2 * q + 1);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) isum[mt][r] += __mul24(s0 - s1, d_lo[r]) + __mul24(s1, d_all[r]);
+                    }
+                }
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    const float xd = f16f((uint16_t)wv[mt].d);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[mt][r] += xd * yd[r] * (float)isum[mt][r];
+                }
+            } else if constexpr (Q == PULSAR_QUANT_Q4_K) {
+                // one MFMA per 32-value sub-block, its 6-bit scale on D; the
+                // min term from two MFMAs on the bsum pair sums split 128 h + l
+                MmaQ4K::W wv[NM];
+                int32_t isum[NM][4];
+                uint32_t mins[NM][2];
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    wv[mt] = MmaQ4K::load_lds(ws + mt * 16u * kRowL, kq);
+                    mins[mt][0] = mins[mt][1] = 0u;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) isum[mt][r] = 0;
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const uint2 a = a_at((uint32_t)t);
+#pragma unroll
+                    for (uint32_t mt = 0; mt < NM; mt++) {
+                        int32_t sc, mn;
+                        Fmt<PULSAR_QUANT_Q4_K>::scale_min(wv[mt].hdr, (uint32_t)t, sc, mn);
+                        mins[mt][t >> 2] |= (uint32_t)mn << (8 * (t & 3));
+                        const v4i d = mfma16x16x32(a, MmaQ4K::codes(wv[mt], t));
+#pragma unroll
+                        for (int r = 0; r < 4; r++) isum[mt][r] += __mul24(sc, d[r]);
+                    }
+                }
+                const uint4 bs = *(const uint4 *)(rec + 272u + 16u * (kq & 1u));
+                const uint2 alh = make_uint2(pair_sum_bytes(bs, kq >= 2u), 0u);
+#pragma unroll
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    const uint32_t mw = mins[mt][kq & 1u];
+                    const v4i dl = mfma16x16x32(alh, kq < 2u ? make_uint2(mw, 0u) : make_uint2(0u, 0u));
+                    const v4i dh = mfma16x16x32(alh, kq < 2u ? make_uint2(0u, 0u) : make_uint2(mw, 0u));
+                    const float xd = f16f((uint16_t)wv[mt].hdr.x), xmin = f16f((uint16_t)(wv[mt].hdr.x >> 16));
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int32_t msum = dl[r] + 128 * dh[r];
+                        acc[mt][r] += xd * yd[r] * (float)isum[mt][r] - xmin * yd[r] * (float)msum;
+                    }
+                }
             } else if constexpr (!kIq2) {
                 uint4 sc[NM];
                 uint2 qv[NM][2];
@@ -721,6 +816,8 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                 if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
                 if (F::kTailBytes == 4u)
                     *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+                else if (F::kTailBytes == 2u)
+                    *(uint16_t *)(wl_w + tdst[j]) = (uint16_t)tv[j];
                 else
                     wl_w[tdst[j]] = (uint8_t)tv[j];
             }
@@ -762,7 +859,9 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
 int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
                           const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
                           uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
-    if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS && quant != PULSAR_QUANT_MXFP4) return -1;
+    if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS && quant != PULSAR_QUANT_MXFP4 &&
+        quant != PULSAR_QUANT_Q4_K && quant != PULSAR_QUANT_Q6_K)
+        return -1;
     const uint32_t k_blocks = (k_dim + 255u) / 256u;
     const uint32_t lim = quant == PULSAR_QUANT_MXFP4 ? k_dim / 32u : k_blocks;
     const uint32_t per_pair = k_blocks * kActLdsPitch;
@@ -786,6 +885,14 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
         PK_GQ(PULSAR_QUANT_IQ2_XXS, true);
     else if (quant == PULSAR_QUANT_IQ2_XXS)
         PK_GQ(PULSAR_QUANT_IQ2_XXS, false);
+    else if (quant == PULSAR_QUANT_Q4_K && pair)
+        PK_GQ(PULSAR_QUANT_Q4_K, true);
+    else if (quant == PULSAR_QUANT_Q4_K)
+        PK_GQ(PULSAR_QUANT_Q4_K, false);
+    else if (quant == PULSAR_QUANT_Q6_K && pair)
+        PK_GQ(PULSAR_QUANT_Q6_K, true);
+    else if (quant == PULSAR_QUANT_Q6_K)
+        PK_GQ(PULSAR_QUANT_Q6_K, false);
     else if (pair)
         PK_GQ(PULSAR_QUANT_MXFP4, true);
     else

@@ -154,13 +154,15 @@ def test_pair_down_decode_shapes(dev):
     check_pair_down(L, ACT_SILU)
 
 
-@pytest.mark.parametrize("gq,n_tok", [(QUANT_Q2_K, 16), (QUANT_IQ2_XXS, 16), (QUANT_Q2_K, 40),
-                                       (QUANT_IQ2_XXS, 40)])
-def test_grouped_mfma_kquants(dev, gq, n_tok):
-    """Q2_K / IQ2_XXS groups run on the matrix cores: pair and down against
-    the oracle (more than 16 pairs per group at n_tok 40: several pair
-    tiles), NULL slots, the slot sum in slot order."""
-    L = Layer(gq, gq, hidden=1024, ffn=512, E=6, n_used=4, n_tok=n_tok, null_slots=(3, 17))
+@pytest.mark.parametrize("gq,dq,n_tok", [(QUANT_Q2_K, QUANT_Q2_K, 16), (QUANT_IQ2_XXS, QUANT_IQ2_XXS, 16),
+                                          (QUANT_Q2_K, QUANT_Q2_K, 40), (QUANT_IQ2_XXS, QUANT_IQ2_XXS, 40),
+                                          (QUANT_Q4_K, QUANT_Q6_K, 16), (QUANT_Q4_K, QUANT_Q6_K, 40),
+                                          (QUANT_Q6_K, QUANT_Q4_K, 24)])
+def test_grouped_mfma_kquants(dev, gq, dq, n_tok):
+    """K-quant / IQ2_XXS groups run on the matrix cores: pair and down
+    against the oracle (more than 16 pairs per group at n_tok 40: several
+    pair tiles), NULL slots, the slot sum in slot order."""
+    L = Layer(gq, dq, hidden=1024, ffn=512, E=6, n_used=4, n_tok=n_tok, null_slots=(3, 17))
     hptrs, dptrs, xq, want_mid, midq, want_out = check_pair_down(L, ACT_SILU)
     ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
     gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
@@ -176,7 +178,7 @@ def test_grouped_mfma_kquants(dev, gq, n_tok):
             assert not got_mid[si].any()  # NULL slots are not in any group: rows stay zero
     partial = zeros_f32((L.n_tok * L.n_used, L.hidden))
     K.moe_down_grouped(partial, gptrs, up(starts), up(pairs), up(midq), L.ffn, L.hidden, L.n_used, len(ids),
-                       L.drb, gq)
+                       L.drb, dq)
     out = zeros_f32((L.n_tok, L.hidden))
     K.moe_slot_sum(out, partial, L.hidden, L.n_used, L.n_tok)
     err = np.abs(down(out).astype(np.float64) - want_out)
@@ -190,7 +192,7 @@ def test_grouped_mfma_kquants(dev, gq, n_tok):
     assert np.array_equal(down(out), acc)
 
 
-@pytest.mark.parametrize("gq", [QUANT_Q2_K, QUANT_IQ2_XXS])
+@pytest.mark.parametrize("gq", [QUANT_Q2_K, QUANT_IQ2_XXS, QUANT_Q4_K, QUANT_Q6_K])
 def test_grouped_mfma_pair_row_tail(dev, gq):
     """A pair stage whose row count (200) is not a multiple of the 16-row
     tile, and 3 super-blocks (768) over the 4 waves' ranges."""
@@ -398,3 +400,20 @@ def test_library_selftests(dev):
     against its host mirrors (the reference ABI's self-test entry points)."""
     assert K.router_selftest()
     assert K.moe_selftest()
+
+
+def test_grouped_wide_rows_lane_fallback(dev):
+    """Rows too wide for the MFMA kernel's staged activations (14336 values:
+    56 q8_K blocks per pair > the 16 KiB tile) run the grouped lane kernels."""
+    L = Layer(QUANT_Q4_K, QUANT_Q6_K, hidden=14336, ffn=256, E=3, n_used=2, n_tok=3)
+    hptrs, dptrs = L.ptrs()
+    xq = oracle.quantize_q8_k(L.x)
+    want_mid = oracle.moe_pair_swiglu(hptrs, L.w, xq, L.hidden, L.ffn, L.n_used, L.n_tok, L.grb, L.gq, ACT_SILU)
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu_grouped(mid, gptrs, up(starts), up(pairs), up_f32(L.w), up(xq), L.hidden, L.ffn,
+                              L.n_used, len(ids), L.grb, QUANT_Q4_K, ACT_SILU)
+    bound = pair_bound(L, xq, ACT_SILU) + 4e-7 * np.abs(want_mid) + 1e-30
+    err = np.abs(down(mid).astype(np.float64) - want_mid)
+    assert (err <= bound).all(), f"grouped pair (lane): max err {err.max():.3e}"
