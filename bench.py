@@ -191,8 +191,11 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
     device routing), "grouped" (router_logits_q8 + moe_route_group + the
     grouped stages + moe_slot_sum[_bias]: six launches), "grouped_split"
     (the same grouped stages behind the reference's separate router, select,
-    pointer and CSR entry points: nine or ten) or "fused" (router_logits_q8 +
-    moe_pair_routed + moe_down_f32: three launches)."""
+    pointer and CSR entry points: nine or ten), "fused" (router_logits_q8 +
+    moe_pair_routed + moe_down_f32: three launches) or "fused_q"
+    (router_logits_q8 + moe_pair_routed + quantize_q8_k + moe_down_biased:
+    four; for wide mid rows, where every fused-down block re-quantizing the
+    token's whole mid costs more than one quantize launch)."""
     torch, K, fm = ctx["torch"], ctx["K"], ctx["fm"]
     s = spec
     bank_bytes = s.n_expert * s.expert_bytes
@@ -226,13 +229,18 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
         b = L.banks[i % n_banks]
         x = xs[i % n_x]
         sel = sel_all[i]
-        if path == "fused":
+        if path in ("fused", "fused_q"):
             K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
             K.moe_pair_routed(mid, ptrs, slot_w, sel, rw, logits, None, s.n_expert, s.k_used, 1.0, 1,
                               descs[i % n_banks], shared[i % n_banks] if shared else None, xq, s.hidden, s.ffn,
                               s.n_tok, s.gate_row_bytes, s.gate_quant, s.act_op)
-            K.moe_down_f32(out, ptrs, slot_w, mid, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
-                           s.down_quant, s.biases)
+            if path == "fused":
+                K.moe_down_f32(out, ptrs, slot_w, mid, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
+                               s.down_quant, s.biases)
+            else:
+                K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
+                K.moe_down_biased(out, ptrs, slot_w, midq, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
+                                  s.down_quant)
             return
         if path == "grouped":
             K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
@@ -437,11 +445,11 @@ def main():
                                                            warmup)
     layer_steps = max(20, steps // 2)
     for spec, path in ((synth.C3, "fused"), (synth.C4_Q2K, "grouped"), (synth.C4_IQ2, "grouped"),
-                       (synth.C5_B1, "fused"), (synth.C5_B64, "grouped")):
+                       (synth.C5_B1, "fused_q"), (synth.C5_B64, "grouped")):
         if on(spec.name):
             results[spec.name] = bench_moe(ctx, spec, layer_steps, warmup, path)
         # the same layer through the reference's own (unfused) entry points
-        if path == "fused" and on(spec.name + "_unfused"):
+        if path.startswith("fused") and on(spec.name + "_unfused"):
             results[spec.name + "_unfused"] = bench_moe(ctx, spec, layer_steps, warmup, "plain")
         if spec is synth.C4_Q2K and on(spec.name + "_split"):
             results[spec.name + "_split"] = bench_moe(ctx, spec, layer_steps, warmup, "grouped_split")

@@ -268,6 +268,11 @@ int pulsar_moe_down_f32(void *out, const void *ptrs, const void *slot_weights, c
                         uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint32_t n_tok,
                         uint64_t row_bytes, uint32_t quant, uint32_t add_bias);
 
+/* pulsar_moe_down + pulsar_moe_down_bias(out, ptrs, weights), one launch. */
+int pulsar_moe_down_biased(void *out, const void *ptrs, const void *weights, const void *midq,
+                           uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint32_t n_tok,
+                           uint64_t row_bytes, uint32_t quant);
+
 /* Selects the stream every later launch from the calling thread goes to
  * (NULL restores the null stream, the default). No counterpart in the
  * reference, whose launches always use the per-thread default stream

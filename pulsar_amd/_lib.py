@@ -42,6 +42,7 @@ SIGNATURES = {
     "pulsar_moe_pair_routed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp, _u32,
                                _vp, _u32, _u32, _u32, _u64, _u32, _u32],
     "pulsar_moe_down_f32": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u64, _u32, _u32],
+    "pulsar_moe_down_biased": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u64, _u32],
     "pulsar_moe_selftest": [],
     "pulsar_router_selftest": [],
 }

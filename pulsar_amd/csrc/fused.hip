@@ -80,7 +80,7 @@ PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expe
 
 // grid (row blocks, k_used + n_shared, n_tok); the pair stage of
 // moe_pair_kernel for the slot's expert, routed in-block.
-template <uint32_t Q, uint32_t UPLMAX, uint32_t J>
+template <uint32_t Q, uint32_t UPLMAX, uint32_t J, uint32_t NPL, uint32_t RPW>
 __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
         float *__restrict__ mid, pulsar_expert_ptrs *__restrict__ ptrs_out, float *__restrict__ slot_w_out,
         int32_t *__restrict__ sel_out, float *__restrict__ w_out, const float *__restrict__ logits,
@@ -96,8 +96,16 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
     // while the wave routes
     Act a[UPLMAX];
     load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
-    const SlotRoute r = route_slot<J>(logits + (uint64_t)token * n_expert, rbias, n_expert, k_used, scale, mode,
-                                      bank, shared, slot);
+    // one wave routes the token for the whole block (every block of the
+    // slot computes the same route)
+    __shared__ SlotRoute route_l;
+    if (threadIdx.x < 64u) {
+        const SlotRoute rr = route_slot<J>(logits + (uint64_t)token * n_expert, rbias, n_expert, k_used, scale,
+                                           mode, bank, shared, slot);
+        if (threadIdx.x == 0) route_l = rr;
+    }
+    __syncthreads();
+    const SlotRoute r = route_l;
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         ptrs_out[so] = r.p;
         slot_w_out[so] = r.w;
@@ -108,25 +116,28 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
     }
     const pulsar_expert_ptrs &p = r.p;
     const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t row = (blockIdx.x * 4u + threadIdx.x / 64u) * rpp + rg.rip;
-    const bool row_ok = row < mid_dim;
+    const uint32_t pass0 = (blockIdx.x * 4u + threadIdx.x / 64u) * RPW;
     if (!p.gate || !p.up) {  // unrouted slot contributes zero (pulsar_kernels.cu:2587-2590)
-        if (row_ok && rg.holds_row()) mid[so * mid_dim + row] = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < RPW; k++) {
+            const uint32_t row = (pass0 + k) * rpp + rg.rip;
+            if (row < mid_dim && rg.holds_row()) mid[so * mid_dim + row] = 0.0f;
+        }
         return;
     }
-    typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
-    load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
-    float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
-    float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
-    if (row_ok && rg.holds_row()) {
-        if (p.gate_b) g += ldwf(p.gate_b + row);
-        if (p.up_b) u += ldwf(p.up_b + row);
-        mid[so * mid_dim + row] = glu(g, u, act_op) * r.w;
-    }
+    pair_passes<Q, UPLMAX, NPL, RPW>(mid + so * mid_dim, p, r.w, a, rg, pass0, mid_dim, row_bytes, act_op, lut);
 }
 
 constexpr uint32_t kFusedMaxPass = 8;  // row passes per block in the fused down
+#ifndef PK_FUSED_DOWN_ROWS
+#define PK_FUSED_DOWN_ROWS 8u
+#endif
+#ifndef PK_FUSED_DOWN_WAVES
+#define PK_FUSED_DOWN_WAVES 16u
+#endif
+// waves of a fused-down block: the token's (pass, slot) dots all in flight
+// at once, and the mid blocks quantized a few per wave
+constexpr uint32_t kFusedDownWaves = PK_FUSED_DOWN_WAVES;
 
 // grid (row blocks, n_tok), a row block = n_pass passes of rpp rows. The
 // block quantizes the token's n_used mid rows into LDS (the q8_K bytes the
@@ -135,8 +146,8 @@ constexpr uint32_t kFusedMaxPass = 8;  // row passes per block in the fused down
 // order from +0 (NULL down: -0, the additive identity) as moe_down_kernel
 // does, then the optional bias term sum_s w_s down_b_s[row] is added when
 // non-zero (moe_down_bias).
-template <uint32_t Q, uint32_t UPLMAX>
-__global__ __launch_bounds__(256) void moe_down_f32_kernel(
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL>
+__global__ __launch_bounds__(1024) void moe_down_f32_kernel(
         float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ ptrs, const float *__restrict__ slot_w,
         const float *__restrict__ mid, uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2,
         uint32_t mid_blocks, uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint64_t row_bytes,
@@ -145,15 +156,15 @@ __global__ __launch_bounds__(256) void moe_down_f32_kernel(
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ pulsar_expert_ptrs p_l[kFusedMaxSlots];
     __shared__ float w_l[kFusedMaxSlots];
-    const uint32_t token = blockIdx.y, wave = threadIdx.x / 64u;
+    const uint32_t token = blockIdx.y, wave = threadIdx.x / 64u, nw = blockDim.x / 64u;
     const uint32_t n_blk = n_used * mid_blocks;
     float *part = (float *)(acts_lds + n_blk * kActLdsPitch);  // [n_pass][n_used][16]
-    // the wave's mid blocks blk = wave + 4i, loaded four at a time before use
-    for (uint32_t base = wave; base < n_blk; base += 16u) {
+    // the wave's mid blocks blk = wave + nw i, loaded four at a time before use
+    for (uint32_t base = wave; base < n_blk; base += 4u * nw) {
         float v[4][4];
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t blk = base + 4u * i;
+            const uint32_t blk = base + nw * i;
             if (blk < n_blk) {
                 const uint32_t s = blk / mid_blocks, b = blk - s * mid_blocks;
                 load_block4(mid + ((uint64_t)token * n_used + s) * mid_dim, mid_dim, b, v[i]);
@@ -161,7 +172,7 @@ __global__ __launch_bounds__(256) void moe_down_f32_kernel(
         }
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t blk = base + 4u * i;
+            const uint32_t blk = base + nw * i;
             if (blk < n_blk) quantize_vals_wave<16u, 272u>(v[i], acts_lds + blk * kActLdsPitch);
         }
     }
@@ -174,7 +185,7 @@ __global__ __launch_bounds__(256) void moe_down_f32_kernel(
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t act_bytes = mid_blocks * kActLdsPitch;
     const uint32_t pass0 = blockIdx.x * n_pass;
-    for (uint32_t ks = wave; ks < n_pass * n_used; ks += 4u) {
+    for (uint32_t ks = wave; ks < n_pass * n_used; ks += nw) {
         const uint32_t k = ks / n_used, s = ks - k * n_used;
         const uint32_t row = (pass0 + k) * rpp + rg.rip;
         if ((pass0 + k) * rpp >= out_dim) break;  // wave-uniform; later items are later passes
@@ -182,7 +193,8 @@ __global__ __launch_bounds__(256) void moe_down_f32_kernel(
         float v = -0.0f;
         if (p_l[s].down) {
             typename Fmt<Q>::W w[UPLMAX];
-            load_row_w<Q, UPLMAX>(as_global(p_l[s].down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
+            load_one_row<Q, UPLMAX, NPL, kFusedDownWaves>(
+                as_global(p_l[s].down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
             Act a[UPLMAX];
             load_row_acts_lds<Q, UPLMAX>(acts_lds + s * act_bytes, rg, a);
             v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
@@ -251,11 +263,20 @@ struct PairRoutedLaunch {
     SharedSlots shared;
     uint64_t row_bytes;
     FGeo g;
-    template <uint32_t Q, uint32_t U, uint32_t J>
+    uint32_t j_per_lane;
+    template <uint32_t Q, uint32_t U, uint32_t NPL>
     int go() {
+        if (j_per_lane == 4u) return go_j<Q, U, 4, NPL>();
+        if (j_per_lane == 8u) return go_j<Q, U, 8, NPL>();
+        return go_j<Q, U, 16, NPL>();
+    }
+    // one row pass per wave: two (as the plain pair kernel takes on large
+    // launches) measured slower here, the routing being on every block's path
+    template <uint32_t Q, uint32_t U, uint32_t J, uint32_t NPL>
+    int go_j() {
         const uint32_t rpb = 4u * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_slots, n_tok);
-        hipLaunchKernelGGL((moe_pair_routed_kernel<Q, U, J>), grid, dim3(256), 0, pk::stream(), (float *)mid,
+        hipLaunchKernelGGL((moe_pair_routed_kernel<Q, U, J, NPL, 1>), grid, dim3(256), 0, pk::stream(), (float *)mid,
                            (pulsar_expert_ptrs *)ptrs_out, (float *)slot_w_out, (int32_t *)sel_out,
                            (float *)w_out, (const float *)logits, (const float *)rbias, n_expert, k_used, scale,
                            mode, bank, shared, (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2,
@@ -264,9 +285,8 @@ struct PairRoutedLaunch {
     }
     template <uint32_t Q, uint32_t U>
     int run() {
-        if (n_expert <= 256u) return go<Q, U, 4>();
-        if (n_expert <= 512u) return go<Q, U, 8>();
-        return go<Q, U, 16>();
+        j_per_lane = n_expert <= 256u ? 4u : n_expert <= 512u ? 8u : 16u;
+        return with_stage<Q, U>(g, *this);
     }
 };
 
@@ -278,13 +298,19 @@ struct DownF32Launch {
     FGeo g;
     template <uint32_t Q, uint32_t U>
     int run() {
+        return with_stage<Q, U>(g, *this);
+    }
+    template <uint32_t Q, uint32_t U, uint32_t NPL>
+    int go() {
         const uint32_t rpp = 64u >> g.l2;
-        uint32_t n_pass = 8u / rpp;  // ~8 rows per block
+        uint32_t n_pass = PK_FUSED_DOWN_ROWS / rpp;  // ~PK_FUSED_DOWN_ROWS rows per block
         n_pass = n_pass < 1u ? 1u : n_pass > kFusedMaxPass ? kFusedMaxPass : n_pass;
         const uint32_t rpb = n_pass * rpp;
         const dim3 grid((out_dim + rpb - 1u) / rpb, n_tok);
         const size_t lds = (size_t)n_used * g.blocks * kActLdsPitch + (size_t)n_pass * n_used * 16u * 4u;
-        hipLaunchKernelGGL((moe_down_f32_kernel<Q, U>), grid, dim3(256), lds, pk::stream(), (float *)out,
+        uint32_t nw = n_pass * n_used;  // one (pass, slot) dot per wave where it fits
+        nw = nw < 4u ? 4u : nw > kFusedDownWaves ? kFusedDownWaves : nw;
+        hipLaunchKernelGGL((moe_down_f32_kernel<Q, U, NPL>), grid, dim3(64u * nw), lds, pk::stream(), (float *)out,
                            (const pulsar_expert_ptrs *)ptrs, (const float *)slot_w, (const float *)mid, g.n_units,
                            g.nblk32, g.l2, g.blocks, mid_dim, out_dim, n_used, row_bytes, add_bias, n_pass);
         return launch_ok("moe down f32 launch");

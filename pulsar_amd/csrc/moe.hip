@@ -17,6 +17,10 @@
 namespace pk {
 
 constexpr uint32_t kWaves = 4;      // waves per block
+#ifndef PK_PAIR_ONE_ROUND
+#define PK_PAIR_ONE_ROUND 2048u
+#endif
+constexpr uint32_t kPairOneRoundBlocks = PK_PAIR_ONE_ROUND;
 constexpr uint32_t kSlotChunk = 32; // down-stage slots staged in LDS per round
 
 #define PK_IQ2_LUT(Q)                                               \
@@ -26,7 +30,10 @@ constexpr uint32_t kSlotChunk = 32; // down-stage slots staged in LDS per round
         __syncthreads();                                            \
     }
 
-template <uint32_t Q, uint32_t UPLMAX>
+// One block per (RPW row-pass groups, slot, token); each wave takes RPW
+// consecutive passes, the next pass's loads in flight while one is
+// computed. NPL > 0: MXFP4 rows staged through LDS (SpanStage).
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t RPW>
 __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
                                                        const pulsar_expert_ptrs *__restrict__ ptrs,
                                                        const float *__restrict__ weights,
@@ -41,36 +48,31 @@ __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
     const pulsar_expert_ptrs p = ptrs[so];
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t row = (blockIdx.x * kWaves + threadIdx.x / 64u) * rpp + rg.rip;
-    const bool row_ok = row < mid_dim;
+    const uint32_t pass0 = (blockIdx.x * kWaves + threadIdx.x / 64u) * RPW;
     if (!p.gate || !p.up) {  // unrouted slot contributes zero (pulsar_kernels.cu:2587-2590)
-        if (row_ok && rg.holds_row()) mid[so * mid_dim + row] = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < RPW; k++) {
+            const uint32_t row = (pass0 + k) * rpp + rg.rip;
+            if (row < mid_dim && rg.holds_row()) mid[so * mid_dim + row] = 0.0f;
+        }
         return;
     }
     Act a[UPLMAX];
     load_row_acts<Q, UPLMAX>(xq + (uint64_t)token * in_blocks, rg, a);
-    typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
-    load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wg);
-    load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, wu);
-    float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wg, a, lut), rg);
-    float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, wu, a, lut), rg);
-    if (row_ok && rg.holds_row()) {
-        // bias on the projection output, then the combine, then the router
-        // weight (pulsar_kernels.cu:2606-2612)
-        if (p.gate_b) g += ldwf(p.gate_b + row);
-        if (p.up_b) u += ldwf(p.up_b + row);
-        mid[so * mid_dim + row] = glu(g, u, act_op) * weights[so];
-    }
+    pair_passes<Q, UPLMAX, NPL, RPW>(mid + so * mid_dim, p, weights[so], a, rg, pass0, mid_dim, row_bytes, act_op,
+                                     lut);
 }
 
-template <uint32_t Q, uint32_t UPLMAX>
+// BIAS: the row total then gets sum_s weights[s] * down_b_s[row] added when
+// that sum is non-zero, as moe_down_bias does after the down stage.
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, bool BIAS>
 __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                                                        const pulsar_expert_ptrs *__restrict__ ptrs,
                                                        const pulsar_block_q8_K *__restrict__ midq,
                                                        uint32_t n_units, uint32_t nblk32,
                                                        uint32_t lpr_log2, uint32_t mid_blocks,
                                                        uint32_t out_dim, uint32_t n_used,
-                                                       uint64_t row_bytes) {
+                                                       uint64_t row_bytes, const float *__restrict__ weights) {
     PK_IQ2_LUT(Q)
     __shared__ float part[kSlotChunk][16];
     const uint32_t token = blockIdx.y;
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                 Act a[UPLMAX];
                 load_row_acts<Q, UPLMAX>(midq + so * mid_blocks, rg, a);
                 typename Fmt<Q>::W w[UPLMAX];
-                load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
+                load_one_row<Q, UPLMAX, NPL>(as_global(p.down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
                 v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
             }
             if (rg.holds_row()) part[s - base][rg.rip] = v;
@@ -102,7 +104,18 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
             for (uint32_t s = base; s < end; s++) total += part[s - base][rg.rip];
         __syncthreads();
     }
-    if (wave == 0 && rg.holds_row() && row_ok) out[(uint64_t)token * out_dim + row] = total;
+    if (wave == 0 && rg.holds_row() && row_ok) {
+        if constexpr (BIAS) {
+            float b = 0.0f;
+            for (uint32_t s = 0; s < n_used; s++) {
+                const uint64_t so = (uint64_t)token * n_used + s;
+                const float *db = ptrs[so].down_b;
+                if (db) b += weights[so] * ldwf(db + row);
+            }
+            if (b != 0.0f) total += b;
+        }
+        out[(uint64_t)token * out_dim + row] = total;
+    }
 }
 
 #ifndef PK_GRP_PPW
@@ -383,12 +396,25 @@ struct PairLaunch {
     Geo g;
     template <uint32_t Q, uint32_t U>
     int run() {
+        return with_stage<Q, U>(g, *this);
+    }
+    template <uint32_t Q, uint32_t U, uint32_t NPL>
+    int go() {
         const uint32_t rpb = kWaves * (64u >> g.l2);
-        const dim3 grid((mid_dim + rpb - 1u) / rpb, n_used, n_tok);
-        hipLaunchKernelGGL((moe_pair_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)mid,
-                           (const pulsar_expert_ptrs *)ptrs, (const float *)weights,
-                           (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
-                           mid_dim, n_used, row_bytes, act_op);
+        // two passes per wave once the blocks would not all be resident at
+        // once (8 per CU): then the waves run as one round
+        const bool two = (uint64_t)((mid_dim + rpb - 1u) / rpb) * n_used * n_tok > kPairOneRoundBlocks;
+        const uint32_t rpw = two ? 2u : 1u;
+        const dim3 grid((mid_dim + rpw * rpb - 1u) / (rpw * rpb), n_used, n_tok);
+#define PK_PAIR_GO(R)                                                                                          \
+    hipLaunchKernelGGL((moe_pair_kernel<Q, U, NPL, R>), grid, dim3(256), 0, pk::stream(), (float *)mid,       \
+                       (const pulsar_expert_ptrs *)ptrs, (const float *)weights, (const pulsar_block_q8_K *)xq, \
+                       g.n_units, g.nblk32, g.l2, g.blocks, mid_dim, n_used, row_bytes, act_op)
+        if (two)
+            PK_PAIR_GO(2);
+        else
+            PK_PAIR_GO(1);
+#undef PK_PAIR_GO
         return launch_ok("moe pair swiglu launch");
     }
 };
@@ -399,13 +425,23 @@ struct DownLaunch {
     uint32_t out_dim, n_used, n_tok;
     uint64_t row_bytes;
     Geo g;
+    const float *weights = nullptr;  // != NULL: bias epilogue (moe_down_kernel BIAS)
     template <uint32_t Q, uint32_t U>
     int run() {
+        return with_stage<Q, U>(g, *this);
+    }
+    template <uint32_t Q, uint32_t U, uint32_t NPL>
+    int go() {
         const uint32_t rpp = 64u >> g.l2;
         const dim3 grid((out_dim + rpp - 1u) / rpp, n_tok);
-        hipLaunchKernelGGL((moe_down_kernel<Q, U>), grid, dim3(256), 0, pk::stream(), (float *)out,
-                           (const pulsar_expert_ptrs *)ptrs, (const pulsar_block_q8_K *)midq,
-                           g.n_units, g.nblk32, g.l2, g.blocks, out_dim, n_used, row_bytes);
+        if (weights)
+            hipLaunchKernelGGL((moe_down_kernel<Q, U, NPL, true>), grid, dim3(256), 0, pk::stream(), (float *)out,
+                               (const pulsar_expert_ptrs *)ptrs, (const pulsar_block_q8_K *)midq, g.n_units,
+                               g.nblk32, g.l2, g.blocks, out_dim, n_used, row_bytes, weights);
+        else
+            hipLaunchKernelGGL((moe_down_kernel<Q, U, NPL, false>), grid, dim3(256), 0, pk::stream(), (float *)out,
+                               (const pulsar_expert_ptrs *)ptrs, (const pulsar_block_q8_K *)midq, g.n_units,
+                               g.nblk32, g.l2, g.blocks, out_dim, n_used, row_bytes, nullptr);
         return launch_ok("moe down launch");
     }
 };
@@ -477,6 +513,20 @@ extern "C" int pulsar_moe_down(void *out, const void *ptrs, const void *midq, ui
     const Geo g = geo_for(quant, mid_dim);
     DownLaunch f{out, ptrs, midq, out_dim, n_used, n_tok, row_bytes, g};
     if (!quant_ok(quant)) return reject("moe down (quant)");
+    return with_format<8>(quant, g.upl, f);
+}
+
+extern "C" int pulsar_moe_down_biased(void *out, const void *ptrs, const void *weights, const void *midq,
+                                      uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint32_t n_tok,
+                                      uint64_t row_bytes, uint32_t quant) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    if (!out || !ptrs || !weights || !midq || mid_dim == 0 || out_dim == 0 || n_used == 0 || n_tok == 0 ||
+        row_bytes == 0 || n_tok > 65535u)
+        return reject("moe down biased");
+    const Geo g = geo_for(quant, mid_dim);
+    DownLaunch f{out, ptrs, midq, out_dim, n_used, n_tok, row_bytes, g};
+    f.weights = (const float *)weights;
+    if (!quant_ok(quant)) return reject("moe down biased (quant)");
     return with_format<8>(quant, g.upl, f);
 }
 

@@ -97,6 +97,14 @@ PK_DEV uint32_t ldw32(const uint8_t *p) { return *(const PK_GLOBAL u32_u *)p; }
 PK_DEV uint16_t ldw16(const uint8_t *p) { return *(const PK_GLOBAL u16_u *)p; }
 PK_DEV uint32_t ldw8(const uint8_t *p) { return *(const PK_GLOBAL uint8_t *)p; }
 PK_DEV float ldwf(const float *p) { return *(const PK_GLOBAL float *)p; }
+#define PK_LDS __attribute__((address_space(3)))
+// 16 bytes from LDS at any byte offset: gfx950 DS reads accept unaligned
+// addresses (one ds_read_b128).
+PK_DEV uint4 lds128u(const uint8_t *p) {
+    const u32x4_u v = *(const PK_LDS u32x4_u *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+PK_DEV uint32_t lds8(const uint8_t *p) { return *(const PK_LDS uint8_t *)p; }
 PK_DEV uint16_t ld16(const uint8_t *p) {
     uint16_t v;
     __builtin_memcpy(&v, p, 2);

@@ -441,6 +441,17 @@ struct Fmt<PULSAR_QUANT_MXFP4> {
         w.e = ldw8(p) | ((w.two ? ldw8(p1) : 0u) << 8);
         return w;
     }
+    // the same unit from an LDS copy of the row (row = the row's first byte)
+    PK_DEV static W load_lds(const uint8_t *row, uint32_t g, uint32_t n_blocks) {
+        const uint8_t *p = row + 34u * g;
+        W w;
+        w.two = 2u * g + 1u < n_blocks ? 1u : 0u;
+        const uint8_t *p1 = w.two ? p + 17 : p;
+        w.q0 = lds128u(p + 1);
+        w.q1 = lds128u(p1 + 1);
+        w.e = lds8(p) | ((w.two ? lds8(p1) : 0u) << 8);
+        return w;
+    }
     // sumf += scale_half(e) * sumi for each block with sumi != 0, in block order
     PK_DEV static Part part(const W &w, const Act &a, uint32_t, const uint2 *) {
         const int32_t s0 = mxfp4_block(w.q0, a.q[0], a.q[1]);

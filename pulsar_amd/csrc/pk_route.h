@@ -28,13 +28,21 @@ PK_DEV uint32_t score_key(float v) {
     return ((u & 0x80000000u) ? ~u : (u | 0x80000000u)) + 1u;
 }
 
+// Wave maximum, returned wave-uniform: DPP moves carry it to lane 63
+// (row_shr 1/2/4/8 within each 16-lane row, then row_bcast 15/31 across
+// rows; lanes without a source read 0, the identity of an unsigned max),
+// which is read back as a scalar. No LDS-routed permutes: a top-k round
+// is latency-bound on this reduction.
 PK_DEV uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (uint32_t s = 1; s < 64u; s <<= 1) {
-        const uint32_t o = (uint32_t)partner((int32_t)v, s);
-        v = o > v ? o : v;
-    }
-    return v;
+    int32_t x = (int32_t)v;
+    auto mx = [](int32_t a, int32_t b) { return (uint32_t)a > (uint32_t)b ? a : b; };
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane(x, 63);
 }
 
 // The k rounds of the reference's top-k (pulsar_kernels.cu:938-1010) for
@@ -53,16 +61,28 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
     const uint32_t kNegInf = score_key(-INFINITY);
     uint32_t key[J];
     float prob[J];
+    // every load issued before any is used (clamped in-range indices, no
+    // branch around them): a load under a branch makes the compiler wait
+    // for it right there, and these come from memory the previous launch
+    // wrote, at full memory latency each
+    float raw_l[J], bias_l[J];
+    const float *bsrc = bias ? bias : lg;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane * J + j, ec = e < n_expert ? e : n_expert - 1u;
+        raw_l[j] = lg[ec];
+        bias_l[j] = bsrc[ec];
+    }
 #pragma unroll
     for (uint32_t j = 0; j < J; j++) {
         const uint32_t e = lane * J + j;
         win[j] = -1;
         wprob[j] = 0.0f;
         if (e < n_expert) {
-            const float raw = lg[e];
+            const float raw = raw_l[j];
             const float p = mode == 1u ? raw : router_sigmoid(raw);
             prob[j] = mode == 2u ? raw : p;  // mode 2 weights use the raw winner logit
-            key[j] = score_key(p + (bias ? bias[e] : 0.0f));
+            key[j] = score_key(p + (bias ? bias_l[j] : 0.0f));
         } else {
             prob[j] = 0.0f;
             key[j] = 0u;

@@ -130,6 +130,169 @@ PK_DEV void load_row_w(const uint8_t *row, const RowGeom &rg, typename Fmt<Q>::W
     }
 }
 
+// ------------------------------------------------ MXFP4 row staging --
+// MXFP4 rows are runs of 17-byte blocks, so a lane's unit (two blocks)
+// starts at an odd byte and its 16-byte loads straddle 16-byte lines: on
+// 2880-wide expert rows such loads move the slab at ~3.0 TB/s where aligned
+// 16-byte pieces of the same rows move at ~4.7 TB/s. A wave that holds one
+// row (64 lanes per row) copies the row's byte span into its LDS area as
+// aligned pieces, NPL per lane (clamped to the span, so every lane issues
+// every load), and its lanes then read their units from LDS.
+template <uint32_t NPL>
+struct SpanStage {
+    uint4 v[NPL];
+    uint32_t skew, np;
+    PK_DEV void issue(const uint8_t *row, uint32_t nbytes) {
+        const uintptr_t a = (uintptr_t)row;
+        skew = (uint32_t)(a & 15u);
+        np = (skew + nbytes + 15u) >> 4;
+        const uint8_t *a0 = row - skew;
+        const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+        for (uint32_t j = 0; j < NPL; j++) {
+            const uint32_t p = lane + 64u * j;
+            v[j] = ldw128(a0 + 16u * (p < np ? p : np - 1u));
+        }
+    }
+    // Writes the pieces to the wave's area (NPL KiB, 16-byte aligned) and
+    // returns the LDS address of the row's first byte.
+    PK_DEV const uint8_t *store(uint8_t *lds) const {
+        const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+        for (uint32_t j = 0; j < NPL; j++) {
+            const uint32_t p = lane + 64u * j;
+            if (p < np) *(uint4 *)(lds + 16u * p) = v[j];
+        }
+        return lds + skew;
+    }
+};
+
+// Stores of a wave to its own LDS area become visible to its other lanes.
+PK_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The lane's units of a row staged by SpanStage (load_row_w's unit choice).
+template <uint32_t UPLMAX>
+PK_DEV void load_row_w_lds(const uint8_t *row, const RowGeom &rg, Fmt<PULSAR_QUANT_MXFP4>::W (&w)[UPLMAX]) {
+#pragma unroll
+    for (uint32_t i = 0; i < UPLMAX; i++) {
+        const uint32_t g = rg.lir + (i << rg.lpr_log2);
+        w[i] = Fmt<PULSAR_QUANT_MXFP4>::load_lds(row, g < rg.n_units ? g : rg.n_units - 1u, rg.nblk32);
+    }
+}
+
+// The lane's units of one row (NPL == 0: load_row_w; else staged through
+// the wave's NPL KiB of LDS; blocks of at most MAXW waves).
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t MAXW = 4>
+PK_DEV void load_one_row(const uint8_t *row, const RowGeom &rg, typename Fmt<Q>::W (&w)[UPLMAX]) {
+    if constexpr (NPL == 0) {
+        load_row_w<Q, UPLMAX>(row, rg, w);
+    } else {
+        __shared__ __align__(16) uint8_t stage[MAXW][NPL * 1024u];
+        SpanStage<NPL> st;
+        st.issue(row, 17u * rg.nblk32);
+        const uint8_t *l = st.store(stage[threadIdx.x / 64u]);
+        wave_lds_sync();
+        load_row_w_lds<UPLMAX>(l, rg, w);
+        wave_lds_sync();  // read before the wave's next staging overwrites them
+    }
+}
+
+// A wave's gate / up row pair, one pass ahead: issue() starts the loads
+// of the next pass (into registers: the units, or for NPL > 0 the aligned
+// pieces of the MXFP4 rows), land() makes them the current units wg / wu
+// (through the wave's 2 NPL KiB of LDS when staged). The loads of pass k+1
+// are in flight while pass k is computed.
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL>
+struct PairRowPipe {
+    typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
+    typename Fmt<Q>::W ng[NPL ? 1 : UPLMAX], nu[NPL ? 1 : UPLMAX];
+    SpanStage<NPL ? NPL : 1> sg, su;
+    PK_DEV void issue(const uint8_t *grow, const uint8_t *urow, const RowGeom &rg) {
+        if constexpr (NPL == 0) {
+            load_row_w<Q, UPLMAX>(grow, rg, ng);
+            load_row_w<Q, UPLMAX>(urow, rg, nu);
+        } else {
+            sg.issue(grow, 17u * rg.nblk32);
+            su.issue(urow, 17u * rg.nblk32);
+        }
+    }
+    PK_DEV void land(const RowGeom &rg) {
+        if constexpr (NPL == 0) {
+#pragma unroll
+            for (uint32_t i = 0; i < UPLMAX; i++) {
+                wg[i] = ng[i];
+                wu[i] = nu[i];
+            }
+        } else {
+            __shared__ __align__(16) uint8_t stage[4][2][NPL * 1024u];
+            uint8_t(&mine)[2][NPL * 1024u] = stage[threadIdx.x / 64u];
+            const uint8_t *lg = sg.store(mine[0]);
+            const uint8_t *lu = su.store(mine[1]);
+            wave_lds_sync();
+            load_row_w_lds<UPLMAX>(lg, rg, wg);
+            load_row_w_lds<UPLMAX>(lu, rg, wu);
+            wave_lds_sync();  // read before the next land() overwrites them
+        }
+    }
+};
+
+// The pair stage of RPW consecutive row passes of one (token, slot):
+// mid_row[row] = glu(gate . x + gate_b, up . x + up_b) * w for the wave's
+// rows (pulsar_kernels.cu:2606-2612: bias on the projection output, then
+// the combine, then the router weight).
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t RPW>
+PK_DEV void pair_passes(float *mid_row, const pulsar_expert_ptrs &p, float w, const Act (&a)[UPLMAX],
+                        const RowGeom &rg, uint32_t pass0, uint32_t mid_dim, uint64_t row_bytes, uint32_t act_op,
+                        const uint2 *lut) {
+    const uint32_t rpp = 64u >> rg.lpr_log2;
+    PairRowPipe<Q, UPLMAX, NPL> pipe;
+    auto off = [&](uint32_t k) {
+        const uint32_t row = (pass0 + k) * rpp + rg.rip;
+        return (uint64_t)(row < mid_dim ? row : 0u) * row_bytes;
+    };
+    pipe.issue(as_global(p.gate) + off(0), as_global(p.up) + off(0), rg);
+    pipe.land(rg);
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        if (k + 1u < RPW) pipe.issue(as_global(p.gate) + off(k + 1u), as_global(p.up) + off(k + 1u), rg);
+        const uint32_t row = (pass0 + k) * rpp + rg.rip;
+        const bool row_ok = row < mid_dim;
+        float g = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, pipe.wg, a, lut), rg);
+        float u = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, pipe.wu, a, lut), rg);
+        if (row_ok && rg.holds_row()) {
+            if (p.gate_b) g += ldwf(p.gate_b + row);
+            if (p.up_b) u += ldwf(p.up_b + row);
+            mid_row[row] = glu(g, u, act_op) * w;
+        }
+        if (k + 1u < RPW) pipe.land(rg);
+    }
+}
+
+// Pieces per lane for staging an MXFP4 row of nblk32 blocks with UPLMAX
+// units per lane, or 0 when the row is not staged (several rows per wave,
+// or wider than the instantiated staging).
+static inline uint32_t mx_stage_npl(uint32_t quant, uint32_t lpr_log2, uint32_t upl, uint32_t nblk32) {
+    if (quant != PULSAR_QUANT_MXFP4 || lpr_log2 != 6u || upl > 2u) return 0;
+    const uint32_t need = (17u * nblk32 + 30u + 1023u) / 1024u;
+    return need <= 2u * upl ? 2u * upl : need <= 2u * upl + 1u ? 2u * upl + 1u : 0u;
+}
+
+// F::template go<Q, U, NPL>() with the MXFP4 staging depth for the
+// geometry g (l2, nblk32; NPL 0: units loaded from global memory directly).
+template <uint32_t Q, uint32_t U, typename G, typename F>
+static int with_stage(const G &g, F &f) {
+    if constexpr (Q == PULSAR_QUANT_MXFP4 && U <= 2u) {
+        const uint32_t npl = mx_stage_npl(Q, g.l2, U, g.nblk32);
+        if (npl == 2u * U) return f.template go<Q, U, 2u * U>();
+        if (npl == 2u * U + 1u) return f.template go<Q, U, 2u * U + 1u>();
+    }
+    return f.template go<Q, U, 0>();
+}
+
 // This lane's share of the row value: the last lane of each super-block
 // quad holds that super-block's value, every other lane 0. All lanes must
 // call it (it exchanges across lanes).

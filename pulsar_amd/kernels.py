@@ -214,6 +214,13 @@ def moe_down_f32(out, ptrs, slot_weights, mid, mid_dim: int, out_dim: int, n_use
                                            n_used, n_tok, row_bytes, quant, int(bool(add_bias))), "moe_down_f32")
 
 
+def moe_down_biased(out, ptrs, weights, midq, mid_dim: int, out_dim: int, n_used: int, n_tok: int, row_bytes: int,
+                    quant: int) -> None:
+    """moe_down + moe_down_bias in one launch."""
+    _check(_lib.load().pulsar_moe_down_biased(_ptr(out), _ptr(ptrs), _ptr(weights), _ptr(midq), mid_dim, out_dim,
+                                              n_used, n_tok, row_bytes, quant), "moe_down_biased")
+
+
 def moe_selftest() -> bool:
     """pulsar_moe_selftest (klib:1563): the MoE path per format against host mirrors."""
     return bool(_lib.load().pulsar_moe_selftest())

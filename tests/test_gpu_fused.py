@@ -23,6 +23,8 @@ CASES = [
     (QUANT_MXFP4, QUANT_MXFP4, 576, 320, 8, 4, 3, 0, 1, ACT_SWIGLU_OAI, True, True, False),
     (QUANT_Q2_K, QUANT_IQ2_XXS, 512, 512, 40, 6, 2, 0, 0, ACT_SILU, False, False, True),
     (QUANT_IQ2_XXS, QUANT_Q2_K, 256, 768, 300, 5, 4, 2, 1, ACT_SILU, False, True, True),
+    # the c5 batch-1 shape (MXFP4 rows staged through LDS)
+    (QUANT_MXFP4, QUANT_MXFP4, 2880, 2880, 6, 4, 1, 0, 1, ACT_SWIGLU_OAI, True, True, False),
 ]
 
 
@@ -87,6 +89,18 @@ def test_fused_layer_matches_separate_calls(dev, case):
         assert np.array_equal(ga.view(np.uint8), gb.view(np.uint8)), name
     assert np.isfinite(down(b["out"])[: n_tok - 1]).all()
 
+    # pair_routed + quantize + down_biased (the MXFP4 decode path)
+    c = bufs()
+    K.router_logits_q8(c["logits"], c["xq"], x, wr, lb, hidden, E, n_tok)
+    K.moe_pair_routed(c["mid"], c["ptrs"], c["slot_w"], c["sel"], c["rw"], c["logits"], sb, E, k, 1.25, mode,
+                      bank, shared, c["xq"], hidden, ffn, n_tok, L.grb, gq, act)
+    K.quantize_q8_k(c["midq"], c["mid"], ffn, n_tok * n_slots)
+    K.moe_down_biased(c["out"], c["ptrs"], c["slot_w"], c["midq"], ffn, hidden, n_slots, n_tok, L.drb, dq)
+    torch.cuda.synchronize()
+    for name in ("logits", "xq", "sel", "rw", "ptrs", "slot_w", "mid", "midq", "out"):
+        ga, gc = down(a[name]), down(c[name])
+        assert np.array_equal(ga.view(np.uint8), gc.view(np.uint8)), name
+
 
 def test_fused_error_contract(dev):
     buf = torch.zeros(1 << 16, dtype=torch.uint8, device=dev)
@@ -103,6 +117,8 @@ def test_fused_error_contract(dev):
         K.moe_down_f32(buf, buf, None, buf, 256, 256, 4, 1, 210, QUANT_Q6_K, True)
     with pytest.raises(K.KernelError):
         K.router_logits_q8(buf, buf, buf, buf, None, 0, 8, 1)
+    with pytest.raises(K.KernelError):
+        K.moe_down_biased(buf, buf, None, buf, 256, 256, 2, 1, 210, QUANT_Q6_K)
     torch.cuda.synchronize()
 
 

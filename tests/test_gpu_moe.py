@@ -147,6 +147,18 @@ def test_pair_down_mxfp4_tails_biases_oai(dev, hidden, ffn):
     assert np.array_equal(down(d_out), want)
 
 
+@pytest.mark.parametrize("gq,dq,hidden,ffn,E,n_used,n_tok", [
+    (QUANT_MXFP4, QUANT_MXFP4, 2880, 2880, 6, 4, 1),  # the c5 batch-1 shape
+    (QUANT_Q4_K, QUANT_Q6_K, 512, 2048, 10, 8, 5),
+])
+def test_pair_two_passes_per_wave(dev, gq, dq, hidden, ffn, E, n_used, n_tok):
+    """Launches of more than 2048 pair blocks run two row passes per wave
+    (the second pass's loads in flight during the first)."""
+    mx = gq == QUANT_MXFP4
+    L = Layer(gq, dq, hidden=hidden, ffn=ffn, E=E, n_used=n_used, n_tok=n_tok, biases=mx, null_slots=(2,))
+    check_pair_down(L, ACT_SWIGLU_OAI if mx else ACT_SILU)
+
+
 def test_pair_down_decode_shapes(dev):
     """The c3 shape (hidden 2048, FFN 512, 8 routed + 1 shared slot) at a
     reduced expert count."""
