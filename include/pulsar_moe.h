@@ -26,14 +26,29 @@
 extern "C" {
 #endif
 
-/* Quant codes (crates/kernels/src/lib.rs:55-73; pulsar_kernels.cu:2649-2668).
- * This library implements the five expert formats of the hot path; the
- * other reference codes (3, 5-11, 13-17) are rejected with a 0 return. */
+/* Quant codes (crates/kernels/src/lib.rs:55-73; pulsar_kernels.cu:2649-2668),
+ * every one the reference defines. Bytes per 256 values: Q2_K 84, IQ2_XXS 66,
+ * Q4_K 144, Q5_K 176, Q6_K 210, Q3_K 110, IQ2_XS 74, IQ3_XXS 98, Q4_0 8 x 18,
+ * Q5_1 8 x 24, Q8_0 8 x 34, IQ4_XS 136, MXFP4 8 x 17, IQ4_NL 8 x 18, IQ3_S
+ * 110, IQ2_S 82, IQ1_S 50, NVFP4 4 x 36 (crates/gguf/src/lib.rs:145-172). */
 #define PULSAR_QUANT_Q2_K     0u
 #define PULSAR_QUANT_IQ2_XXS  1u
 #define PULSAR_QUANT_Q4_K     2u
+#define PULSAR_QUANT_Q5_K     3u
 #define PULSAR_QUANT_Q6_K     4u
+#define PULSAR_QUANT_Q3_K     5u
+#define PULSAR_QUANT_IQ2_XS   6u
+#define PULSAR_QUANT_IQ3_XXS  7u
+#define PULSAR_QUANT_Q4_0     8u
+#define PULSAR_QUANT_Q5_1     9u
+#define PULSAR_QUANT_Q8_0    10u
+#define PULSAR_QUANT_IQ4_XS  11u
 #define PULSAR_QUANT_MXFP4   12u
+#define PULSAR_QUANT_IQ4_NL  13u
+#define PULSAR_QUANT_IQ3_S   14u
+#define PULSAR_QUANT_IQ2_S   15u
+#define PULSAR_QUANT_IQ1_S   16u
+#define PULSAR_QUANT_NVFP4   17u
 /* OR'd into `quant` by callers that permit W4A4 (crates/kernels/src/lib.rs:51-55);
  * accepted and ignored here (it only selects an NVFP4 path in the reference). */
 #define PULSAR_QUANT_A4_OK   0x80000000u

@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include "../include/pulsar_iq2xxs_grid.h"
+#include "../include/pulsar_iq_grids.h"
 
 /* ---------------------------------------------------------------- f16 -- */
 
@@ -117,22 +118,81 @@ void po_quantize_q8_K(pulsar_block_q8_K *out, const float *x, uint32_t in_dim, u
 
 /* ------------------------------------------------------------ formats -- */
 
+/* bytes per 256 values (crates/gguf/src/lib.rs:145-172) */
 uint32_t po_sb_bytes(uint32_t quant) {
     switch (quant) {
     case PULSAR_QUANT_Q2_K: return 84;
     case PULSAR_QUANT_IQ2_XXS: return 66;
     case PULSAR_QUANT_Q4_K: return 144;
+    case PULSAR_QUANT_Q5_K: return 176;
     case PULSAR_QUANT_Q6_K: return 210;
+    case PULSAR_QUANT_Q3_K: return 110;
+    case PULSAR_QUANT_IQ2_XS: return 74;
+    case PULSAR_QUANT_IQ3_XXS: return 98;
+    case PULSAR_QUANT_Q4_0: return 8 * 18;
+    case PULSAR_QUANT_Q5_1: return 8 * 24;
+    case PULSAR_QUANT_Q8_0: return 8 * 34;
+    case PULSAR_QUANT_IQ4_XS: return 136;
     case PULSAR_QUANT_MXFP4: return 8 * 17;
+    case PULSAR_QUANT_IQ4_NL: return 8 * 18;
+    case PULSAR_QUANT_IQ3_S: return 110;
+    case PULSAR_QUANT_IQ2_S: return 82;
+    case PULSAR_QUANT_IQ1_S: return 50;
+    case PULSAR_QUANT_NVFP4: return 4 * 36;
     default: return 0;
     }
 }
 
 /* crates/gguf/src/lib.rs:145-180: ceil(n / block) * block_bytes; MXFP4 is
- * (32, 17), so its rows pack exact 32-value blocks. */
+ * (32, 17), so its rows pack exact 32-value blocks. Every other format's
+ * rows here are whole 256-value super-blocks. */
 uint64_t po_row_bytes(uint32_t quant, uint32_t n) {
     if (quant == PULSAR_QUANT_MXFP4) return (uint64_t)((n + 31u) / 32u) * 17u;
     return (uint64_t)((n + 255u) / 256u) * po_sb_bytes(quant);
+}
+
+/* cpu:133-145 (k3_unpack_scales): 16 6-bit scales from 12 bytes, minus 32 */
+static void k3_scales(const uint8_t *s, int32_t sc[16]) {
+    for (uint32_t j = 0; j < 16; j++) {
+        const uint32_t hi = ((uint32_t)s[8 + j % 4] >> (2 * (j / 4))) & 3u;
+        const uint32_t lo = j < 8 ? (s[j] & 0x0fu) : (uint32_t)(s[j - 8] >> 4);
+        sc[j] = (int32_t)(lo | (hi << 4)) - 32;
+    }
+}
+
+/* the IQ grids of include/pulsar_iq_grids.h, expanded (signed int8 bytes) */
+static const uint16_t k_iq2xs_codes[512] = {PULSAR_IQ2XS_GRID_CODES};
+static const uint16_t k_iq2s_codes[1024] = {PULSAR_IQ2S_GRID_CODES};
+static const uint16_t k_iq3xxs_codes[256] = {PULSAR_IQ3XXS_GRID_CODES};
+static const uint16_t k_iq3s_codes[512] = {PULSAR_IQ3S_GRID_CODES};
+static const uint16_t k_iq1s_codes[2048] = {PULSAR_IQ1S_GRID_CODES};
+static int32_t base3_digit(uint32_t c, uint32_t j) {
+    for (uint32_t k = 0; k < j; k++) c /= 3u;
+    return (int32_t)(c % 3u);
+}
+static int32_t iq2xs_mag(uint32_t idx, uint32_t j) {
+    static const int32_t m[3] = {8, 25, 43};
+    return m[base3_digit(k_iq2xs_codes[idx], j)];
+}
+static int32_t iq2s_mag(uint32_t idx, uint32_t j) {
+    static const int32_t m[3] = {8, 25, 43};
+    return m[base3_digit(k_iq2s_codes[idx], j)];
+}
+static int32_t iq3xxs_mag(uint32_t idx, uint32_t j) {
+    static const int32_t m[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+    return m[(k_iq3xxs_codes[idx] >> (3 * j)) & 7u];
+}
+static int32_t iq3s_mag(uint32_t idx, uint32_t j) { return 2 * (int32_t)((k_iq3s_codes[idx] >> (3 * j)) & 7u) + 1; }
+static int32_t iq1s_val(uint32_t idx, uint32_t j) { return base3_digit(k_iq1s_codes[idx], j) - 1; }
+
+/* cu:5602-5603, 5843 (kvalues_iq4nl) */
+static const int32_t k_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* cu:5762-5767 (ggml_ue4m3_to_fp32): unsigned E4M3, 0 and 0x7F are zero */
+static float ue4m3(uint8_t e) {
+    if (e == 0 || e == 0x7F) return 0.0f;
+    const int ex = (e >> 3) & 0xF, man = e & 7;
+    return ex == 0 ? ldexpf((float)man, -9) : ldexpf(1.0f + (float)man / 8.0f, ex - 7);
 }
 
 /* cpu:147-156 == cu:1349-1359 (ggml get_scale_min_k4) */
@@ -315,6 +375,295 @@ float po_block_dot(uint32_t quant, const uint8_t *row, uint32_t b,
         f = yd * sumf;
         break;
     }
+    case PULSAR_QUANT_Q5_K: {
+        /* cu:5892-5918: Q4_K with a fifth bit per value from qh (bit 2j of
+         * qh[i] for value 64j + i, bit 2j + 1 for 64j + 32 + i) */
+        const uint8_t *blk = row + (uint64_t)b * 176u;
+        const float xd = po_f16_to_f32(rd16(blk));
+        const float xmin = po_f16_to_f32(rd16(blk + 2));
+        const uint8_t *qh = blk + 16, *q5 = blk + 48;
+        int32_t isum = 0, msum = 0;
+        for (uint32_t j = 0; j < 4; j++) {
+            int32_t sc1, m1, sc2, m2;
+            k4_scale_min(2 * j, blk + 4, &sc1, &m1);
+            k4_scale_min(2 * j + 1, blk + 4, &sc2, &m2);
+            int32_t s1 = 0, s2 = 0;
+            for (uint32_t i = 0; i < 32; i++) {
+                const int32_t h1 = (qh[i] >> (2 * j)) & 1, h2 = (qh[i] >> (2 * j + 1)) & 1;
+                s1 += ((q5[32 * j + i] & 0x0f) | (h1 << 4)) * q8[64 * j + i];
+                s2 += ((q5[32 * j + i] >> 4) | (h2 << 4)) * q8[64 * j + 32 + i];
+            }
+            isum += sc1 * s1 + sc2 * s2;
+            msum += m1 * (bs[4 * j] + bs[4 * j + 1]) + m2 * (bs[4 * j + 2] + bs[4 * j + 3]);
+        }
+        d0 = isum;
+        d1 = msum;
+        f = xd * yd * (float)isum - xmin * yd * (float)msum;
+        break;
+    }
+    case PULSAR_QUANT_Q3_K: {
+        /* cpu:166-204 (== cu:5807-5838) */
+        const uint8_t *blk = row + (uint64_t)b * 110u;
+        const uint8_t *hm = blk, *q3 = blk + 32;
+        const float xd = po_f16_to_f32(rd16(blk + 108));
+        int32_t sc[16];
+        k3_scales(blk + 96, sc);
+        int32_t isum = 0;
+        uint32_t hbit = 1u, is = 0;
+        for (uint32_t k = 0; k < 2; k++) {
+            for (uint32_t shift = 0; shift < 8; shift += 2) {
+                for (uint32_t half = 0; half < 2; half++) {
+                    int32_t s16 = 0;
+                    for (uint32_t i = 0; i < 16; i++) {
+                        const uint32_t l = 16 * half + i;
+                        int32_t q = (q3[32 * k + l] >> shift) & 3;
+                        if ((hm[l] & hbit) == 0u) q -= 4;
+                        s16 += q * q8[128 * k + 32 * (shift / 2) + l];
+                    }
+                    isum += sc[is++] * s16;
+                }
+                hbit <<= 1;
+            }
+        }
+        d0 = isum;
+        f = xd * yd * (float)isum;
+        break;
+    }
+    case PULSAR_QUANT_IQ2_XS: {
+        /* cpu:299-338 */
+        const uint8_t *blk = row + (uint64_t)b * 74u;
+        const float xd = po_f16_to_f32(rd16(blk));
+        int32_t bsum = 0;
+        for (uint32_t g = 0; g < 8; g++) {
+            const uint8_t sc = blk[66 + g];
+            const int32_t ls1 = 2 * (sc & 0x0f) + 1, ls2 = 2 * (sc >> 4) + 1;
+            int32_t s1 = 0, s2 = 0;
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t q = rd16(blk + 2 + 2 * (4 * g + j));
+                const uint32_t sm = sign_mask(q >> 9);
+                int32_t acc = 0;
+                for (uint32_t i = 0; i < 8; i++) {
+                    const int32_t gv = iq2xs_mag(q & 511u, i);
+                    acc += ((sm >> i) & 1u ? -gv : gv) * q8[32 * g + 8 * j + i];
+                }
+                if (j < 2) s1 += acc; else s2 += acc;
+            }
+            bsum += ls1 * s1 + ls2 * s2;
+        }
+        d0 = bsum;
+        f = 0.125f * xd * yd * (float)bsum;
+        break;
+    }
+    case PULSAR_QUANT_IQ3_XXS: {
+        /* cpu:349-390: per group db = xd * (0.5 + s) * 0.5 in f32;
+         * d0 = sum_g (2 s + 1) * sumi_g, the same value in integers */
+        const uint8_t *blk = row + (uint64_t)b * 98u;
+        const float xd = po_f16_to_f32(rd16(blk));
+        float sumf = 0.0f;
+        int32_t isum = 0;
+        for (uint32_t g = 0; g < 8; g++) {
+            const uint32_t aux = rd32(blk + 66 + 4 * g);
+            const float db = xd * (0.5f + (float)(aux >> 28)) * 0.5f;
+            int32_t sumi = 0;
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t sm = sign_mask((aux >> (7 * j)) & 127u);
+                const uint32_t i0 = blk[2 + 8 * g + 2 * j], i1 = blk[2 + 8 * g + 2 * j + 1];
+                for (uint32_t i = 0; i < 4; i++) {
+                    const int32_t w0 = iq3xxs_mag(i0, i), w1 = iq3xxs_mag(i1, i);
+                    sumi += ((sm >> i) & 1u ? -w0 : w0) * q8[32 * g + 8 * j + i] +
+                            ((sm >> (4 + i)) & 1u ? -w1 : w1) * q8[32 * g + 8 * j + 4 + i];
+                }
+            }
+            sumf += db * (float)sumi;
+            isum += (int32_t)(2u * (aux >> 28) + 1u) * sumi;
+        }
+        d0 = isum;
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_IQ4_XS: {
+        /* cu:5843-5865 */
+        const uint8_t *blk = row + (uint64_t)b * 136u;
+        const uint32_t sh = rd16(blk + 2);
+        const uint8_t *qs = blk + 8;
+        float sumf = 0.0f;
+        int any = 0;
+        int32_t isum = 0;
+        for (uint32_t ib = 0; ib < 8; ib++) {
+            const int32_t ls = (int32_t)(((blk[4 + ib / 2] >> (4 * (ib & 1))) & 0x0fu) | (((sh >> (2 * ib)) & 3u) << 4)) - 32;
+            int32_t sumi = 0;
+            for (uint32_t j = 0; j < 16; j++) {
+                const uint8_t v = qs[16 * ib + j];
+                sumi += k_iq4nl[v & 0x0f] * q8[32 * ib + j] + k_iq4nl[v >> 4] * q8[32 * ib + 16 + j];
+            }
+            if (sumi != 0) {
+                sumf += (float)(ls * sumi);
+                any = 1;
+            }
+            isum += ls * sumi;
+        }
+        d0 = isum;
+        f = any ? po_f16_to_f32(rd16(blk)) * yd * sumf : 0.0f;
+        break;
+    }
+    case PULSAR_QUANT_Q8_0: {
+        /* cu:5793-5805: 8 blocks of f16 d + 32 int8 */
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint8_t *bp = row + (uint64_t)b * 272u + 34u * k;
+            int32_t sumi = 0;
+            for (uint32_t i = 0; i < 32; i++) sumi += (int8_t)bp[2 + i] * q8[32 * k + i];
+            if (sumi != 0) sumf += po_f16_to_f32(rd16(bp)) * (float)sumi;
+            if (sumi_out) sumi_out[k] = sumi;
+        }
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_Q4_0: {
+        /* cu:5773-5791: value = nibble - 8, folded through the bsums */
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint8_t *bp = row + (uint64_t)b * 144u + 18u * k;
+            int32_t sumi = 0;
+            for (uint32_t i = 0; i < 16; i++)
+                sumi += (bp[2 + i] & 0x0f) * q8[32 * k + i] + (bp[2 + i] >> 4) * q8[32 * k + 16 + i];
+            const int32_t bsum = bs[2 * k] + bs[2 * k + 1];
+            if (sumi != 0 || bsum != 0) sumf += po_f16_to_f32(rd16(bp)) * (float)(sumi - 8 * bsum);
+            if (sumi_out) sumi_out[k] = sumi - 8 * bsum;
+        }
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_Q5_1: {
+        /* cu:5950-5975: value = d * (nibble | qh bit << 4) + m */
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint8_t *bp = row + (uint64_t)b * 192u + 24u * k;
+            const uint32_t qh = rd32(bp + 4);
+            int32_t sumi = 0;
+            for (uint32_t i = 0; i < 16; i++) {
+                const int32_t lo = (bp[8 + i] & 0x0f) | (int32_t)(((qh >> i) & 1u) << 4);
+                const int32_t hi = (bp[8 + i] >> 4) | (int32_t)(((qh >> (i + 16)) & 1u) << 4);
+                sumi += lo * q8[32 * k + i] + hi * q8[32 * k + 16 + i];
+            }
+            const int32_t bsum = bs[2 * k] + bs[2 * k + 1];
+            if (sumi != 0 || bsum != 0)
+                sumf += po_f16_to_f32(rd16(bp)) * (float)sumi + po_f16_to_f32(rd16(bp + 2)) * (float)bsum;
+            if (sumi_out) sumi_out[k] = sumi;
+        }
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_IQ4_NL: {
+        /* cu:5605-5625 */
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint8_t *bp = row + (uint64_t)b * 144u + 18u * k;
+            int32_t sumi = 0;
+            for (uint32_t i = 0; i < 16; i++)
+                sumi += k_iq4nl[bp[2 + i] & 0x0f] * q8[32 * k + i] + k_iq4nl[bp[2 + i] >> 4] * q8[32 * k + 16 + i];
+            if (sumi != 0) sumf += po_f16_to_f32(rd16(bp)) * (float)sumi;
+            if (sumi_out) sumi_out[k] = sumi;
+        }
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_IQ3_S: {
+        /* cu:5683-5713; d0 = sum_g (1 + 2 sc) * sumi_g */
+        const uint8_t *blk = row + (uint64_t)b * 110u;
+        const float d = po_f16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2, *qhb = blk + 66, *sg = blk + 74, *scb = blk + 106;
+        float sumf = 0.0f;
+        int32_t isum = 0;
+        for (uint32_t g = 0; g < 8; g++) {
+            const int32_t sc = (g & 1) ? (scb[g >> 1] >> 4) : (scb[g >> 1] & 0x0f);
+            const float db = d * (float)(1 + 2 * sc);
+            const uint32_t qh = qhb[g];
+            int32_t sumi = 0;
+            for (uint32_t l = 0; l < 4; l++) {
+                const uint32_t i0 = qs[8 * g + 2 * l] | ((qh << (8 - 2 * l)) & 256u);
+                const uint32_t i1 = qs[8 * g + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256u);
+                const uint32_t s = sg[4 * g + l];
+                for (uint32_t j = 0; j < 4; j++) {
+                    const int32_t v0 = iq3s_mag(i0, j), v1 = iq3s_mag(i1, j);
+                    sumi += ((s >> j) & 1u ? -v0 : v0) * q8[32 * g + 8 * l + j] +
+                            ((s >> (j + 4)) & 1u ? -v1 : v1) * q8[32 * g + 8 * l + 4 + j];
+                }
+            }
+            sumf += db * (float)sumi;
+            isum += (1 + 2 * sc) * sumi;
+        }
+        d0 = isum;
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_IQ2_S: {
+        /* cu:5627-5657; d0 = sum (2 n + 1) * acc, dl = d (2 n + 1) / 8 */
+        const uint8_t *blk = row + (uint64_t)b * 82u;
+        const float d = po_f16_to_f32(rd16(blk));
+        const uint8_t *qs = blk + 2, *sg = blk + 34, *qhb = blk + 66, *scb = blk + 74;
+        float sumf = 0.0f;
+        int32_t isum = 0;
+        for (uint32_t g = 0; g < 8; g++) {
+            const uint32_t qh = qhb[g];
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t idx = qs[4 * g + j] | ((qh << (8 - 2 * j)) & 0x300u);
+                const uint32_t s = sg[4 * g + j];
+                const int32_t n = j < 2 ? (scb[g] & 0x0f) : (scb[g] >> 4);
+                const float dl = d * (0.5f + (float)n) * 0.25f;
+                int32_t acc = 0;
+                for (uint32_t k = 0; k < 8; k++) {
+                    const int32_t gv = iq2s_mag(idx, k);
+                    acc += ((s >> k) & 1u ? -gv : gv) * q8[32 * g + 8 * j + k];
+                }
+                sumf += dl * (float)acc;
+                isum += (2 * n + 1) * acc;
+            }
+        }
+        d0 = isum;
+        f = yd * sumf;
+        break;
+    }
+    case PULSAR_QUANT_IQ1_S: {
+        /* cu:5659-5681 */
+        const uint8_t *blk = row + (uint64_t)b * 50u;
+        int32_t sumi = 0, sumi1 = 0;
+        for (uint32_t g = 0; g < 8; g++) {
+            const uint32_t qh = rd16(blk + 34 + 2 * g);
+            const int32_t ls = 2 * (int32_t)((qh >> 12) & 7u) + 1;
+            const int32_t dsign = (qh & 0x8000u) ? -1 : 1;
+            int32_t lsum = 0;
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t idx = blk[2 + 4 * g + j] | (((qh >> (3 * j)) & 7u) << 8);
+                for (uint32_t k = 0; k < 8; k++) lsum += iq1s_val(idx, k) * q8[32 * g + 8 * j + k];
+            }
+            sumi += ls * lsum;
+            sumi1 += ls * dsign * (bs[2 * g] + bs[2 * g + 1]);
+        }
+        d0 = sumi;
+        d1 = sumi1;
+        f = po_f16_to_f32(rd16(blk)) * yd * ((float)sumi + 0.125f * (float)sumi1);
+        break;
+    }
+    case PULSAR_QUANT_NVFP4: {
+        /* cu:5743-5771: 4 blocks of 4 UE4M3 scales + 32 nibble bytes; per
+         * 16-value sub-block the doubled E2M1 table and half the scale */
+        float sumf = 0.0f;
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint8_t *bp = row + (uint64_t)b * 144u + 36u * k;
+            for (uint32_t sub = 0; sub < 4; sub++) {
+                int32_t sumi = 0;
+                for (uint32_t i = 0; i < 8; i++) {
+                    const uint8_t q = bp[4 + 8 * sub + i];
+                    sumi += k_mxfp4_kv[q & 0x0f] * q8[64 * k + 16 * sub + i] +
+                            k_mxfp4_kv[q >> 4] * q8[64 * k + 16 * sub + 8 + i];
+                }
+                sumf += ue4m3(bp[sub]) * 0.5f * (float)sumi;
+            }
+        }
+        f = yd * sumf;
+        break;
+    }
     default:
         break;
     }
@@ -431,6 +780,170 @@ void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out)
             }
             break;
         }
+        case PULSAR_QUANT_Q5_K: { /* 8 sub-blocks of 32: xd sc q5 - xmin m */
+            const uint8_t *blk = row + (uint64_t)b * 176u;
+            const double xd = po_f16_to_f32(rd16(blk)), xmin = po_f16_to_f32(rd16(blk + 2));
+            for (uint32_t s = 0; s < 8; s++) {
+                int32_t sc, m;
+                k4_scale_min(s, blk + 4, &sc, &m);
+                for (uint32_t i = 0; i < 32; i++) {
+                    const uint8_t byte = blk[48 + 32 * (s / 2) + i];
+                    const int32_t lo = (s & 1) ? (byte >> 4) : (byte & 0x0f);
+                    const int32_t q = lo | (((blk[16 + i] >> s) & 1) << 4);
+                    v[32 * s + i] = xd * sc * q - xmin * m;
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_Q3_K: { /* cpu:921-935: 16-value chunk c = 8k + 2js + half */
+            const uint8_t *blk = row + (uint64_t)b * 110u;
+            const double xd = po_f16_to_f32(rd16(blk + 108));
+            int32_t sc[16];
+            k3_scales(blk + 96, sc);
+            for (uint32_t c = 0; c < 16; c++) {
+                const uint32_t k = c / 8, js = (c % 8) / 2, half = c % 2;
+                for (uint32_t i = 0; i < 16; i++) {
+                    const uint32_t l = 16 * half + i;
+                    int32_t q = (blk[32 + 32 * k + l] >> (2 * js)) & 3;
+                    if ((blk[l] & (1u << (4 * k + js))) == 0) q -= 4;
+                    v[16 * c + i] = xd * sc[c] * q;
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_IQ2_XS: { /* cpu:1008-1022 */
+            const uint8_t *blk = row + (uint64_t)b * 74u;
+            const double xd = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++)
+                for (uint32_t j = 0; j < 4; j++) {
+                    const uint32_t q = rd16(blk + 2 + 2 * (4 * g + j));
+                    const uint32_t sm = sign_mask(q >> 9);
+                    const double ls = j < 2 ? 2 * (blk[66 + g] & 0x0f) + 1 : 2 * (blk[66 + g] >> 4) + 1;
+                    for (uint32_t i = 0; i < 8; i++)
+                        v[32 * g + 8 * j + i] = 0.125 * xd * ls * iq2xs_mag(q & 511u, i) * ((sm >> i) & 1u ? -1.0 : 1.0);
+                }
+            break;
+        }
+        case PULSAR_QUANT_IQ3_XXS: { /* cpu:1050-1073 */
+            const uint8_t *blk = row + (uint64_t)b * 98u;
+            const double xd = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++) {
+                const uint32_t aux = rd32(blk + 66 + 4 * g);
+                const double db = xd * (0.5 + (aux >> 28)) * 0.5;
+                for (uint32_t j = 0; j < 4; j++) {
+                    const uint32_t sm = sign_mask((aux >> (7 * j)) & 127u);
+                    for (uint32_t i = 0; i < 4; i++) {
+                        v[32 * g + 8 * j + i] = db * iq3xxs_mag(blk[2 + 8 * g + 2 * j], i) * ((sm >> i) & 1u ? -1.0 : 1.0);
+                        v[32 * g + 8 * j + 4 + i] =
+                            db * iq3xxs_mag(blk[3 + 8 * g + 2 * j], i) * ((sm >> (4 + i)) & 1u ? -1.0 : 1.0);
+                    }
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_IQ4_XS: { /* d (ls - 32) kvalues[q], ls 6-bit split low 4 / high 2 */
+            const uint8_t *blk = row + (uint64_t)b * 136u;
+            const double xd = po_f16_to_f32(rd16(blk));
+            const uint32_t sh = rd16(blk + 2);
+            for (uint32_t ib = 0; ib < 8; ib++) {
+                const int32_t ls = (int32_t)(((blk[4 + ib / 2] >> (4 * (ib & 1))) & 0x0fu) | (((sh >> (2 * ib)) & 3u) << 4)) - 32;
+                for (uint32_t j = 0; j < 16; j++) {
+                    const uint8_t q = blk[8 + 16 * ib + j];
+                    v[32 * ib + j] = xd * ls * k_iq4nl[q & 0x0f];
+                    v[32 * ib + 16 + j] = xd * ls * k_iq4nl[q >> 4];
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_Q8_0:
+        case PULSAR_QUANT_Q4_0:
+        case PULSAR_QUANT_Q5_1:
+        case PULSAR_QUANT_IQ4_NL: { /* 8 blocks of 32 values with an f16 scale each */
+            const uint32_t bb = quant == PULSAR_QUANT_Q8_0 ? 34u : quant == PULSAR_QUANT_Q5_1 ? 24u : 18u;
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint8_t *bp = row + (uint64_t)b * 8u * bb + (uint64_t)bb * k;
+                const double d = po_f16_to_f32(rd16(bp));
+                for (uint32_t i = 0; i < 32; i++) {
+                    double val;
+                    if (quant == PULSAR_QUANT_Q8_0) {
+                        val = d * (int8_t)bp[2 + i];
+                    } else {
+                        const uint32_t off = quant == PULSAR_QUANT_Q5_1 ? 8u : 2u;
+                        const int32_t nib = i < 16 ? (bp[off + i] & 0x0f) : (bp[off + i - 16] >> 4);
+                        if (quant == PULSAR_QUANT_Q4_0)
+                            val = d * (nib - 8);
+                        else if (quant == PULSAR_QUANT_IQ4_NL)
+                            val = d * k_iq4nl[nib];
+                        else /* value i's fifth bit is bit i of qh */
+                            val = d * (nib | (int32_t)(((rd32(bp + 4) >> i) & 1u) << 4)) + po_f16_to_f32(rd16(bp + 2));
+                    }
+                    v[32 * k + i] = val;
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_IQ3_S: { /* d (1 + 2 sc) +-grid, 9-bit indices, explicit sign bytes */
+            const uint8_t *blk = row + (uint64_t)b * 110u;
+            const double d = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++) {
+                const int32_t sc = (g & 1) ? (blk[106 + g / 2] >> 4) : (blk[106 + g / 2] & 0x0f);
+                for (uint32_t p = 0; p < 8; p++) { /* grid entry p of the group: values 4p .. 4p+3 */
+                    const uint32_t idx = blk[2 + 8 * g + p] | ((((uint32_t)blk[66 + g] >> p) & 1u) << 8);
+                    const uint32_t s = blk[74 + 4 * g + p / 2];
+                    for (uint32_t j = 0; j < 4; j++) {
+                        const uint32_t bit = 4 * (p & 1) + j;
+                        v[32 * g + 4 * p + j] = d * (1 + 2 * sc) * iq3s_mag(idx, j) * ((s >> bit) & 1u ? -1.0 : 1.0);
+                    }
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_IQ2_S: { /* d (0.5 + n) / 4 +-grid, 10-bit indices */
+            const uint8_t *blk = row + (uint64_t)b * 82u;
+            const double d = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++)
+                for (uint32_t j = 0; j < 4; j++) {
+                    const uint32_t idx = blk[2 + 4 * g + j] | ((((uint32_t)blk[66 + g] >> (2 * j)) & 3u) << 8);
+                    const uint32_t s = blk[34 + 4 * g + j];
+                    const int32_t n = j < 2 ? (blk[74 + g] & 0x0f) : (blk[74 + g] >> 4);
+                    for (uint32_t k = 0; k < 8; k++)
+                        v[32 * g + 8 * j + k] = d * (0.5 + n) * 0.25 * iq2s_mag(idx, k) * ((s >> k) & 1u ? -1.0 : 1.0);
+                }
+            break;
+        }
+        case PULSAR_QUANT_IQ1_S: { /* d (2 s + 1) (g +- 1/8), g ternary */
+            const uint8_t *blk = row + (uint64_t)b * 50u;
+            const double d = po_f16_to_f32(rd16(blk));
+            for (uint32_t g = 0; g < 8; g++) {
+                const uint32_t qh = rd16(blk + 34 + 2 * g);
+                const double dl = d * (2 * ((qh >> 12) & 7u) + 1);
+                const double delta = (qh & 0x8000u) ? -0.125 : 0.125;
+                for (uint32_t j = 0; j < 4; j++) {
+                    const uint32_t idx = blk[2 + 4 * g + j] | (((qh >> (3 * j)) & 7u) << 8);
+                    for (uint32_t k = 0; k < 8; k++) v[32 * g + 8 * j + k] = dl * (iq1s_val(idx, k) + delta);
+                }
+            }
+            break;
+        }
+        case PULSAR_QUANT_NVFP4: { /* OCP E2M1 times a UE4M3 scale per 16 values */
+            static const double e2m1[8] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0};
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint8_t *bp = row + (uint64_t)b * 144u + 36u * k;
+                for (uint32_t sub = 0; sub < 4; sub++) {
+                    const uint8_t e = bp[sub];
+                    const int ex = (e >> 3) & 0xF, man = e & 7;
+                    const double scale = (e == 0 || e == 0x7F) ? 0.0
+                                         : ex == 0 ? ldexp((double)man, -9) : ldexp(1.0 + man / 8.0, ex - 7);
+                    for (uint32_t i = 0; i < 8; i++) {
+                        const uint8_t q = bp[4 + 8 * sub + i];
+                        const uint8_t lo = q & 0x0f, hi = q >> 4;
+                        v[64 * k + 16 * sub + i] = (lo & 8 ? -1.0 : 1.0) * e2m1[lo & 7] * scale;
+                        v[64 * k + 16 * sub + 8 + i] = (hi & 8 ? -1.0 : 1.0) * e2m1[hi & 7] * scale;
+                    }
+                }
+            }
+            break;
+        }
         default:
             break;
         }
@@ -441,11 +954,7 @@ void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out)
     }
 }
 
-static int quant_ok(uint32_t quant) {
-    return quant == PULSAR_QUANT_Q2_K || quant == PULSAR_QUANT_IQ2_XXS ||
-           quant == PULSAR_QUANT_Q4_K || quant == PULSAR_QUANT_Q6_K ||
-           quant == PULSAR_QUANT_MXFP4;
-}
+static int quant_ok(uint32_t quant) { return po_sb_bytes(quant) != 0; }
 
 /* cu:4895-4906 argument contract; each output is the lane's row dot */
 int po_matmul_kq(float *out, const uint8_t *w, const pulsar_block_q8_K *xq,
