@@ -22,12 +22,6 @@ namespace pk {
 constexpr uint32_t kFusedMaxSlots = 64;    // k_used + n_shared
 constexpr uint32_t kFusedMaxActLds = 65536; // staged mid rows of one token
 
-#define PK_FUSED_IQ2_LUT(Q)                                         \
-    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];    \
-    if ((Q) == PULSAR_QUANT_IQ2_XXS) {                              \
-        fill_iq2xxs_lut(lut);                                       \
-        __syncthreads();                                            \
-    }
 
 // Blocks [0, gemv_blocks) compute logits (one wave per (row, TG tokens)),
 // the rest quantize x (one wave per 256-value block).
@@ -88,7 +82,7 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
         pulsar_expert_bank bank, SharedSlots shared, const pulsar_block_q8_K *__restrict__ xq, uint32_t n_units,
         uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t mid_dim, uint64_t row_bytes,
         uint32_t act_op) {
-    PK_FUSED_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     const uint32_t slot = blockIdx.y, token = blockIdx.z, n_slots = gridDim.y;
     const uint64_t so = (uint64_t)token * n_slots + slot;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
@@ -152,7 +146,7 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
         const float *__restrict__ mid, uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2,
         uint32_t mid_blocks, uint32_t mid_dim, uint32_t out_dim, uint32_t n_used, uint64_t row_bytes,
         uint32_t add_bias, uint32_t n_pass) {
-    PK_FUSED_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ pulsar_expert_ptrs p_l[kFusedMaxSlots];
     __shared__ float w_l[kFusedMaxSlots];
@@ -243,14 +237,13 @@ static int fused_format(uint32_t quant, uint32_t upl, F &&f) {
     if (upl <= 2u) return f.template run<Q, 2>();        \
     if (upl <= 4u) return f.template run<Q, 4>();        \
     return reject("fused moe (row width above the supported maximum)");
+#define PK_FCASE(Q) \
+    case Q: PK_FUPL(Q)
     switch (quant) {
-    case PULSAR_QUANT_Q2_K: PK_FUPL(PULSAR_QUANT_Q2_K)
-    case PULSAR_QUANT_IQ2_XXS: PK_FUPL(PULSAR_QUANT_IQ2_XXS)
-    case PULSAR_QUANT_Q4_K: PK_FUPL(PULSAR_QUANT_Q4_K)
-    case PULSAR_QUANT_Q6_K: PK_FUPL(PULSAR_QUANT_Q6_K)
-    case PULSAR_QUANT_MXFP4: PK_FUPL(PULSAR_QUANT_MXFP4)
+    PK_FOR_EACH_QUANT(PK_FCASE)
     default: return reject("fused moe (quant)");
     }
+#undef PK_FCASE
 #undef PK_FUPL
 }
 

@@ -31,11 +31,7 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
                                                      uint32_t lpr_log2, uint32_t in_blocks,
                                                      uint32_t out_dim, uint32_t n_tok,
                                                      uint64_t row_bytes, uint32_t n_pass) {
-    __shared__ uint2 lut[Q == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];
-    if (Q == PULSAR_QUANT_IQ2_XXS) {
-        fill_iq2xxs_lut(lut);
-        __syncthreads();
-    }
+    PK_FMT_LUT(Q)
     const RowGeom rg = row_geom<L2>(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> rg.lpr_log2;
     const uint32_t t0 = blockIdx.y * T;
@@ -155,11 +151,20 @@ extern "C" int pulsar_matmul_kq(void *out, const void *w, const void *xq, uint32
         const int r = pk::launch_gemm(quant, o, wb, x, in_dim, out_dim, n_tok, row_bytes);
         if (r >= 0) return r;
     }
+    // the dense formats of pulsar_kernels.cu:5090-5142
+#define PK_MVQ(Q) \
+    case Q: return pk::dispatch_matvec<Q>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
     switch (quant) {
-    case PULSAR_QUANT_Q4_K: return pk::dispatch_matvec<PULSAR_QUANT_Q4_K>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
-    case PULSAR_QUANT_Q6_K: return pk::dispatch_matvec<PULSAR_QUANT_Q6_K>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
-    case PULSAR_QUANT_Q2_K: return pk::dispatch_matvec<PULSAR_QUANT_Q2_K>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
-    case PULSAR_QUANT_IQ2_XXS: return pk::dispatch_matvec<PULSAR_QUANT_IQ2_XXS>(o, wb, x, in_dim, out_dim, n_tok, row_bytes);
+    PK_MVQ(PULSAR_QUANT_Q4_K)
+    PK_MVQ(PULSAR_QUANT_Q6_K)
+    PK_MVQ(PULSAR_QUANT_Q2_K)
+    PK_MVQ(PULSAR_QUANT_IQ2_XXS)
+    PK_MVQ(PULSAR_QUANT_Q5_K)
+    PK_MVQ(PULSAR_QUANT_Q3_K)
+    PK_MVQ(PULSAR_QUANT_IQ4_XS)
+    PK_MVQ(PULSAR_QUANT_IQ4_NL)
+    PK_MVQ(PULSAR_QUANT_NVFP4)
     default: return pk::reject("matmul_kq (quant)");
     }
+#undef PK_MVQ
 }

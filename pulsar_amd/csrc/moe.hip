@@ -23,12 +23,6 @@ constexpr uint32_t kWaves = 4;      // waves per block
 constexpr uint32_t kPairOneRoundBlocks = PK_PAIR_ONE_ROUND;
 constexpr uint32_t kSlotChunk = 32; // down-stage slots staged in LDS per round
 
-#define PK_IQ2_LUT(Q)                                               \
-    __shared__ uint2 lut[(Q) == PULSAR_QUANT_IQ2_XXS ? kIq2LutRows : 1];    \
-    if ((Q) == PULSAR_QUANT_IQ2_XXS) {                              \
-        fill_iq2xxs_lut(lut);                                       \
-        __syncthreads();                                            \
-    }
 
 // One block per (RPW row-pass groups, slot, token); each wave takes RPW
 // consecutive passes, the next pass's loads in flight while one is
@@ -42,7 +36,7 @@ __global__ __launch_bounds__(256) void moe_pair_kernel(float *__restrict__ mid,
                                                        uint32_t lpr_log2, uint32_t in_blocks,
                                                        uint32_t mid_dim, uint32_t n_used,
                                                        uint64_t row_bytes, uint32_t act_op) {
-    PK_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     const uint32_t slot = blockIdx.y, token = blockIdx.z;
     const uint64_t so = (uint64_t)token * n_used + slot;
     const pulsar_expert_ptrs p = ptrs[so];
@@ -73,7 +67,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                                                        uint32_t lpr_log2, uint32_t mid_blocks,
                                                        uint32_t out_dim, uint32_t n_used,
                                                        uint64_t row_bytes, const float *__restrict__ weights) {
-    PK_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     __shared__ float part[kSlotChunk][16];
     const uint32_t token = blockIdx.y;
     const uint32_t wave = threadIdx.x / 64u;
@@ -152,7 +146,7 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
         const float *__restrict__ weights, const pulsar_block_q8_K *__restrict__ xq,
         uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t mid_dim,
         uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
-    PK_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
@@ -229,7 +223,7 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
         const pulsar_block_q8_K *__restrict__ midq, uint32_t n_units, uint32_t nblk32,
         uint32_t lpr_log2, uint32_t mid_blocks, uint32_t out_dim, uint32_t n_used,
         uint64_t row_bytes, uint32_t pmax) {
-    PK_IQ2_LUT(Q)
+    PK_FMT_LUT(Q)
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
@@ -361,10 +355,7 @@ static Geo geo_for(uint32_t quant, uint32_t k_dim) {
     return g;
 }
 
-static bool quant_ok(uint32_t q) {
-    return q == PULSAR_QUANT_Q2_K || q == PULSAR_QUANT_IQ2_XXS || q == PULSAR_QUANT_Q4_K ||
-           q == PULSAR_QUANT_Q6_K || q == PULSAR_QUANT_MXFP4;
-}
+static bool quant_ok(uint32_t q) { return q <= PULSAR_QUANT_NVFP4; }
 
 // Calls F::template run<Q, UPLMAX>() for the run-time (quant, upl);
 // MAXU bounds the instantiated unit counts (the grouped kernels hold two
@@ -377,14 +368,13 @@ static int with_format(uint32_t quant, uint32_t upl, F &&f) {
     if (upl <= 4u) return f.template run<Q, 4>();                   \
     if (MAXU >= 8u && upl <= 8u) return f.template run<Q, (MAXU >= 8u ? 8u : 4u)>(); \
     return reject("moe (row width above the supported maximum)");
+#define PK_CASE(Q) \
+    case Q: PK_UPL(Q)
     switch (quant) {
-    case PULSAR_QUANT_Q2_K: PK_UPL(PULSAR_QUANT_Q2_K)
-    case PULSAR_QUANT_IQ2_XXS: PK_UPL(PULSAR_QUANT_IQ2_XXS)
-    case PULSAR_QUANT_Q4_K: PK_UPL(PULSAR_QUANT_Q4_K)
-    case PULSAR_QUANT_Q6_K: PK_UPL(PULSAR_QUANT_Q6_K)
-    case PULSAR_QUANT_MXFP4: PK_UPL(PULSAR_QUANT_MXFP4)
+    PK_FOR_EACH_QUANT(PK_CASE)
     default: return reject("moe (quant)");
     }
+#undef PK_CASE
 #undef PK_UPL
 }
 

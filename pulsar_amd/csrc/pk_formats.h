@@ -468,3 +468,50 @@ struct Fmt<PULSAR_QUANT_MXFP4> {
 };
 
 }  // namespace pk
+
+#include "pk_formats_ext.h"
+
+namespace pk {
+
+// Per-format LDS table of the lane kernels (kRows uint2 rows; 1 = none)
+// and its fill, by all threads of the block before a __syncthreads().
+template <uint32_t Q, typename = void>
+struct FmtLut {
+    static constexpr uint32_t kRows = 1;
+    PK_DEV static void fill(uint2 *) {}
+};
+template <>
+struct FmtLut<PULSAR_QUANT_IQ2_XXS> {
+    static constexpr uint32_t kRows = kIq2LutRows;
+    PK_DEV static void fill(uint2 *lut) { fill_iq2xxs_lut(lut); }
+};
+template <uint32_t Q>
+struct FmtLut<Q, decltype((void)Fmt<Q>::kLutRows)> {
+    static constexpr uint32_t kRows = Fmt<Q>::kLutRows;
+    PK_DEV static void fill(uint2 *lut) { Fmt<Q>::fill_lut(lut); }
+};
+
+// Formats whose super-block value is a float sum of per-block terms (the
+// unit's float partial is reduced across the quad instead of integers).
+template <uint32_t Q>
+constexpr bool kFloatPart = Q == PULSAR_QUANT_MXFP4 || Q == PULSAR_QUANT_Q8_0 || Q == PULSAR_QUANT_Q4_0 ||
+                            Q == PULSAR_QUANT_Q5_1 || Q == PULSAR_QUANT_IQ4_NL || Q == PULSAR_QUANT_NVFP4;
+
+}  // namespace pk
+
+// Declares and fills the format's LDS table `lut` (every thread of the
+// block must reach it).
+#define PK_FMT_LUT(Q)                                   \
+    __shared__ uint2 lut[pk::FmtLut<Q>::kRows];         \
+    if constexpr (pk::FmtLut<Q>::kRows > 1) {           \
+        pk::FmtLut<Q>::fill(lut);                       \
+        __syncthreads();                                \
+    }
+
+// Switch over every expert format: F(Q) per code.
+#define PK_FOR_EACH_QUANT(F)                                                                    \
+    F(PULSAR_QUANT_Q2_K) F(PULSAR_QUANT_IQ2_XXS) F(PULSAR_QUANT_Q4_K) F(PULSAR_QUANT_Q5_K)      \
+    F(PULSAR_QUANT_Q6_K) F(PULSAR_QUANT_Q3_K) F(PULSAR_QUANT_IQ2_XS) F(PULSAR_QUANT_IQ3_XXS)    \
+    F(PULSAR_QUANT_Q4_0) F(PULSAR_QUANT_Q5_1) F(PULSAR_QUANT_Q8_0) F(PULSAR_QUANT_IQ4_XS)       \
+    F(PULSAR_QUANT_MXFP4) F(PULSAR_QUANT_IQ4_NL) F(PULSAR_QUANT_IQ3_S) F(PULSAR_QUANT_IQ2_S)    \
+    F(PULSAR_QUANT_IQ1_S) F(PULSAR_QUANT_NVFP4)

@@ -319,7 +319,7 @@ PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::
             p.i1 += dpp_shr<1>(p.i1);
             p.i1 += dpp_shr<2>(p.i1);
         }
-        if (Q == PULSAR_QUANT_MXFP4) {
+        if (kFloatPart<Q>) {
             p.f = ok ? p.f : 0.0f;
             p.f += dpp_shr<1>(p.f);
             p.f += dpp_shr<2>(p.f);

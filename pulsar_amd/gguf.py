@@ -82,14 +82,27 @@ BLOCK_LAYOUT = {
     TensorType.MXFP4: (32, 17), TensorType.NVFP4: (64, 36),
 }
 
-# file type -> this library's kernel quant code (the expert formats it runs;
-# crates/engine/src/lib.rs:551-573 maps the wider set of the reference)
+# file type -> kernel quant code (crates/engine/src/lib.rs:551-573: every
+# expert format the reference dispatches)
 QUANT_OF_TYPE = {
-    TensorType.Q2_K: fm.QUANT_Q2_K,
     TensorType.IQ2_XXS: fm.QUANT_IQ2_XXS,
+    TensorType.Q2_K: fm.QUANT_Q2_K,
     TensorType.Q4_K: fm.QUANT_Q4_K,
+    TensorType.Q5_K: fm.QUANT_Q5_K,
     TensorType.Q6_K: fm.QUANT_Q6_K,
+    TensorType.Q3_K: fm.QUANT_Q3_K,
+    TensorType.IQ2_XS: fm.QUANT_IQ2_XS,
+    TensorType.IQ3_XXS: fm.QUANT_IQ3_XXS,
+    TensorType.Q4_0: fm.QUANT_Q4_0,
+    TensorType.Q5_1: fm.QUANT_Q5_1,
+    TensorType.Q8_0: fm.QUANT_Q8_0,
+    TensorType.IQ4_XS: fm.QUANT_IQ4_XS,
+    TensorType.IQ4_NL: fm.QUANT_IQ4_NL,
+    TensorType.IQ3_S: fm.QUANT_IQ3_S,
+    TensorType.IQ2_S: fm.QUANT_IQ2_S,
+    TensorType.IQ1_S: fm.QUANT_IQ1_S,
     TensorType.MXFP4: fm.QUANT_MXFP4,
+    TensorType.NVFP4: fm.QUANT_NVFP4,
 }
 
 

@@ -7,6 +7,9 @@ distributions are the ones the benchmark configurations state:
   Q2_K   : scale/min nibbles and 2-bit qs uniform; f16 d, dmin ~ U[1e-3, 1e-2]
   IQ2_XXS: grid indices, sign bits and 4-bit scales uniform; f16 d ~ U[1e-3, 1e-2]
   MXFP4  : E2M1 codes uniform; E8M0 exponent ~ U{118..126}
+  other formats (parity tests): uniform bytes with every f16 scale
+           ~ U[1e-3, 1e-2] (Q5_1's min with a random sign), NVFP4 UE4M3
+           scales with exponent field 4..10
   activations ~ N(0, 1) fp32; biases ~ N(0, 0.02)
 Everything derives from numpy's PCG64 seeded per tensor, so a (seed, name)
 pair always yields the same bytes.
@@ -19,11 +22,25 @@ from dataclasses import dataclass
 import numpy as np
 
 from .formats import (
+    BLOCK_LAYOUT,
+    QUANT_IQ1_S,
+    QUANT_IQ2_S,
+    QUANT_IQ2_XS,
     QUANT_IQ2_XXS,
+    QUANT_IQ3_S,
+    QUANT_IQ3_XXS,
+    QUANT_IQ4_NL,
+    QUANT_IQ4_XS,
     QUANT_MXFP4,
+    QUANT_NVFP4,
     QUANT_Q2_K,
+    QUANT_Q3_K,
+    QUANT_Q4_0,
     QUANT_Q4_K,
+    QUANT_Q5_1,
+    QUANT_Q5_K,
     QUANT_Q6_K,
+    QUANT_Q8_0,
     row_bytes,
 )
 
@@ -49,9 +66,26 @@ def quant_matrix(quant: int, rows: int, cols: int, rng: np.random.Generator) -> 
         raw = np.frombuffer(rng.bytes(rows * rb), dtype=np.uint8).reshape(rows, nblk, 17).copy()
         raw[..., 0] = rng.integers(118, 127, size=(rows, nblk), dtype=np.uint8)
         return raw.reshape(rows, rb)
-    bb = {QUANT_Q2_K: 84, QUANT_IQ2_XXS: 66, QUANT_Q4_K: 144, QUANT_Q6_K: 210}[quant]
+    bb = BLOCK_LAYOUT[quant][1]
     nb = rb // bb
     raw = np.frombuffer(rng.bytes(rows * rb), dtype=np.uint8).reshape(rows, nb, bb).copy()
+    # every other format: f16 scales uniform in [1e-3, 1e-2] at these offsets
+    # of each block (Q5_1's min with a random sign), NVFP4's UE4M3 scales with
+    # exponent fields 4..10; the remaining bytes stay uniform random
+    d_offs = {QUANT_Q5_K: (0, 2), QUANT_Q3_K: (108,), QUANT_IQ2_XS: (0,), QUANT_IQ3_XXS: (0,), QUANT_IQ4_XS: (0,),
+              QUANT_IQ3_S: (0,), QUANT_IQ2_S: (0,), QUANT_IQ1_S: (0,), QUANT_Q8_0: (0,), QUANT_Q4_0: (0,),
+              QUANT_IQ4_NL: (0,), QUANT_Q5_1: (0,)}
+    if quant in d_offs:
+        for off in d_offs[quant]:
+            _put_u16(raw, off, _f16_uniform(rng, (rows, nb)))
+        if quant == QUANT_Q5_1:
+            m = _f16_uniform(rng, (rows, nb)) | (rng.integers(0, 2, (rows, nb)).astype(np.uint16) << 15)
+            _put_u16(raw, 2, m)
+        return raw.reshape(rows, rb)
+    if quant == QUANT_NVFP4:
+        ex = rng.integers(4, 11, size=(rows, nb, 4), dtype=np.uint8)
+        raw[..., 0:4] = (ex << 3) | rng.integers(0, 8, size=(rows, nb, 4), dtype=np.uint8)
+        return raw.reshape(rows, rb)
     if quant == QUANT_Q4_K:
         _put_u16(raw, 0, _f16_uniform(rng, (rows, nb)))
         _put_u16(raw, 2, _f16_uniform(rng, (rows, nb)))

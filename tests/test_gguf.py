@@ -158,7 +158,7 @@ def test_layer_experts_and_reads(tmp_path):
 def test_expert_errors(tmp_path):
     p = tmp_path / "bad.gguf"
     md = {"general.architecture": "x", "x.expert_count": 2}
-    G.write_gguf(p, md, [("blk.0.ffn_gate_exps.weight", (256, 4, 2), TT.Q5_K, _rand(2 * 4 * 176, 1)),
+    G.write_gguf(p, md, [("blk.0.ffn_gate_exps.weight", (256, 4, 2), TT.Q5_0, _rand(2 * 4 * 176, 1)),
                          ("blk.0.ffn_up_exps.weight", (256, 4, 3), TT.Q4_K, _rand(3 * 4 * 144, 2))])
     g = G.Gguf.open(p)
     with pytest.raises(G.GgufError, match="unsupported expert type"):

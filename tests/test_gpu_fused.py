@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+from pulsar_amd import formats as fm
 from pulsar_amd import kernels as K
 from pulsar_amd.formats import (ACT_SILU, ACT_SWIGLU_OAI, QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K,
                                 QUANT_Q6_K, q8k_blocks)
@@ -23,6 +24,11 @@ CASES = [
     (QUANT_MXFP4, QUANT_MXFP4, 576, 320, 8, 4, 3, 0, 1, ACT_SWIGLU_OAI, True, True, False),
     (QUANT_Q2_K, QUANT_IQ2_XXS, 512, 512, 40, 6, 2, 0, 0, ACT_SILU, False, False, True),
     (QUANT_IQ2_XXS, QUANT_Q2_K, 256, 768, 300, 5, 4, 2, 1, ACT_SILU, False, True, True),
+    # formats beyond the benchmark configurations (LDS grid tables, float partials)
+    (fm.QUANT_Q5_K, fm.QUANT_IQ4_XS, 512, 256, 16, 4, 2, 1, 1, ACT_SILU, False, False, False),
+    (fm.QUANT_IQ1_S, fm.QUANT_NVFP4, 512, 512, 12, 3, 3, 0, 0, ACT_SILU, False, True, True),
+    (fm.QUANT_Q8_0, fm.QUANT_Q3_K, 768, 256, 10, 2, 2, 0, 1, ACT_SWIGLU_OAI, True, False, False),
+    (fm.QUANT_IQ3_S, fm.QUANT_IQ2_S, 256, 512, 8, 4, 1, 1, 1, ACT_SILU, False, False, False),
     # the c5 batch-1 shape (MXFP4 rows staged through LDS)
     (QUANT_MXFP4, QUANT_MXFP4, 2880, 2880, 6, 4, 1, 0, 1, ACT_SWIGLU_OAI, True, True, False),
 ]

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 import oracle
+from pulsar_amd import formats as fm
 from pulsar_amd import kernels as K
 from pulsar_amd import synth
 from pulsar_amd.formats import (ACT_SILU, ACT_SWIGLU_OAI, QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K,
@@ -429,3 +430,43 @@ def test_grouped_wide_rows_lane_fallback(dev):
     bound = pair_bound(L, xq, ACT_SILU) + 4e-7 * np.abs(want_mid) + 1e-30
     err = np.abs(down(mid).astype(np.float64) - want_mid)
     assert (err <= bound).all(), f"grouped pair (lane): max err {err.max():.3e}"
+
+
+NEW_FORMATS = [fm.QUANT_Q5_K, fm.QUANT_Q3_K, fm.QUANT_IQ2_XS, fm.QUANT_IQ3_XXS, fm.QUANT_Q4_0, fm.QUANT_Q5_1,
+               fm.QUANT_Q8_0, fm.QUANT_IQ4_XS, fm.QUANT_IQ4_NL, fm.QUANT_IQ3_S, fm.QUANT_IQ2_S, fm.QUANT_IQ1_S,
+               fm.QUANT_NVFP4]
+
+
+@pytest.mark.parametrize("q", NEW_FORMATS, ids=lambda q: fm.NAMES[q])
+def test_pair_down_every_format(dev, q):
+    """The remaining expert formats (pulsar_kernels.cu:2649-2668) through the
+    plain pair / down stages against the oracle; 3 tokens, a NULL slot, 768
+    inputs (3 super-blocks) and 512 mid values."""
+    L = Layer(q, q, hidden=768, ffn=512, E=6, n_used=4, n_tok=3, null_slots=(5,))
+    check_pair_down(L, ACT_SILU)
+
+
+@pytest.mark.parametrize("q", NEW_FORMATS, ids=lambda q: fm.NAMES[q])
+def test_grouped_every_format(dev, q):
+    """The same formats through the grouped entry points (lane kernels)."""
+    L = Layer(q, q, hidden=512, ffn=256, E=5, n_used=4, n_tok=12, null_slots=(7,))
+    hptrs, dptrs = L.ptrs()
+    xq = oracle.quantize_q8_k(L.x)
+    want_mid = oracle.moe_pair_swiglu(hptrs, L.w, xq, L.hidden, L.ffn, L.n_used, L.n_tok, L.grb, q, ACT_SILU)
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu_grouped(mid, gptrs, up(starts), up(pairs), up_f32(L.w), up(xq), L.hidden, L.ffn,
+                              L.n_used, len(ids), L.grb, q, ACT_SILU)
+    bound = pair_bound(L, xq, ACT_SILU) + 4e-7 * np.abs(want_mid) + 1e-30
+    err = np.abs(down(mid).astype(np.float64) - want_mid)
+    assert (err <= bound).all(), f"grouped pair: max err {err.max():.3e}"
+    midq = oracle.quantize_q8_k(want_mid)
+    partial = zeros_f32((L.n_tok * L.n_used, L.hidden))
+    K.moe_down_grouped(partial, gptrs, up(starts), up(pairs), up(midq), L.ffn, L.hidden, L.n_used, len(ids),
+                       L.drb, q)
+    out = zeros_f32((L.n_tok, L.hidden))
+    K.moe_slot_sum(out, partial, L.hidden, L.n_used, L.n_tok)
+    want = oracle.moe_down(hptrs, midq, L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, q)
+    err = np.abs(down(out).astype(np.float64) - want)
+    assert (err <= down_bound(L, midq)).all(), f"grouped down: max err {err.max():.3e}"

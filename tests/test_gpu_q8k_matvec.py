@@ -6,6 +6,7 @@ import torch
 
 import oracle
 from pulsar_amd import kernels as K
+from pulsar_amd import formats as fm
 from pulsar_amd import synth
 from pulsar_amd.formats import QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K, QUANT_Q6_K, row_bytes
 from tests.gpu_util import assert_rows_close, down, up, up_f32, zeros_f32, zeros_u8
@@ -63,10 +64,11 @@ def unit_scale_xq(n_tok: int, n: int) -> np.ndarray:
 
 def unit_scale_matrix(quant, rows, n, seed):
     w = synth.quant_matrix(quant, rows, n, synth.rng_for(seed, "unit"))
-    bb = {QUANT_Q4_K: 144, QUANT_Q2_K: 84, QUANT_Q6_K: 210, QUANT_IQ2_XXS: 66}[quant]
+    bb = fm.BLOCK_LAYOUT[quant][1]
     blk = w.reshape(rows, -1, bb)
     d_off, m_off, d_val = {QUANT_Q4_K: (0, 2, 0x3C00), QUANT_Q2_K: (80, 82, 0x3C00), QUANT_Q6_K: (208, None, 0x3C00),
-                           QUANT_IQ2_XXS: (0, None, 0x4800)}[quant]
+                           QUANT_IQ2_XXS: (0, None, 0x4800), fm.QUANT_Q5_K: (0, 2, 0x3C00),
+                           fm.QUANT_Q3_K: (108, None, 0x3C00)}[quant]
     blk[..., d_off], blk[..., d_off + 1] = d_val & 0xFF, d_val >> 8
     if m_off is not None:
         blk[..., m_off], blk[..., m_off + 1] = 0x00, 0x3C  # dmin = 1
@@ -155,3 +157,47 @@ def test_matvec_error_contract(dev):
     xq = zeros_u8(292)
     K.matmul_kq(out, buf, xq, 256, 4, 1, 144, QUANT_Q4_K | 0x8000_0000)
     torch.cuda.synchronize()
+
+
+MORE_DENSE = [fm.QUANT_Q5_K, fm.QUANT_Q3_K, fm.QUANT_IQ4_XS, fm.QUANT_IQ4_NL, fm.QUANT_NVFP4]
+
+
+@pytest.mark.parametrize("quant", [fm.QUANT_Q5_K, fm.QUANT_Q3_K], ids=lambda q: fm.NAMES[q])
+@pytest.mark.parametrize("n,rows,n_tok", [(256, 37, 1), (2048, 64, 1), (4096, 33, 3), (1024, 16, 5), (512, 33, 40)])
+def test_matvec_more_formats_integer_exact(dev, quant, n, rows, n_tok):
+    """Q5_K and Q3_K dense dots at unit scales: exact integers, bit-exact."""
+    w = unit_scale_matrix(quant, rows, n, n + rows)
+    xq = unit_scale_xq(n_tok, n)
+    rb = row_bytes(quant, n)
+    out = zeros_f32((n_tok, rows))
+    K.matmul_kq(out, up(w), up(xq), n, rows, n_tok, rb, quant)
+    want = oracle.matmul_kq(w, xq, n, rows, n_tok, rb, quant)
+    assert np.abs(want).max() < 2**24
+    assert np.array_equal(down(out), want)
+
+
+@pytest.mark.parametrize("quant", MORE_DENSE, ids=lambda q: fm.NAMES[q])
+@pytest.mark.parametrize("n,rows,n_tok", [(256, 5, 1), (2048, 130, 1), (4096, 40, 3), (4096, 24, 16), (1024, 50, 64)])
+def test_matvec_more_formats_fp32_parity(dev, quant, n, rows, n_tok):
+    """The other dense formats of pulsar_kernels.cu:5090-5142 against the
+    oracle, decode and token chunks."""
+    w = synth.quant_matrix(quant, rows, n, synth.rng_for(n * rows + n_tok, "mv2"))
+    x = rng.standard_normal((n_tok, n)).astype(np.float32)
+    xq = oracle.quantize_q8_k(x)
+    rb = row_bytes(quant, n)
+    out = zeros_f32((n_tok, rows))
+    K.matmul_kq(out, up(w), up(xq), n, rows, n_tok, rb, quant)
+    got = down(out)
+    for t in range(n_tok):
+        vals, scale = zip(*(oracle.vec_dot(quant, w[r], xq[t], n) for r in range(rows)))
+        assert_rows_close(got[t], np.array(vals, np.float32), np.array(scale), f"q{quant} n{n} t{t}")
+
+
+def test_matvec_rejects_moe_only_formats(dev):
+    """Q4_0, Q5_1, Q8_0 and the IQ1-3 formats are expert formats only: the
+    dense entry point returns 0 for them (pulsar_kernels.cu:5110, 5139)."""
+    buf = up(np.zeros(1 << 16, np.uint8))
+    for q in (fm.QUANT_Q4_0, fm.QUANT_Q5_1, fm.QUANT_Q8_0, fm.QUANT_IQ2_XS, fm.QUANT_IQ3_XXS, fm.QUANT_IQ3_S,
+              fm.QUANT_IQ2_S, fm.QUANT_IQ1_S, fm.QUANT_MXFP4):
+        with pytest.raises(K.KernelError):
+            K.matmul_kq(buf, buf, buf, 256, 4, 1, row_bytes(q, 256), q)
