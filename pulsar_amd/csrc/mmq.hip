@@ -125,6 +125,12 @@ struct GemmFmt<PULSAR_QUANT_Q4_K> {
     static constexpr uint32_t kSb = 144, kChunks = 9, kDSlot = 0;
     static constexpr bool kBsums = true;
 };
+// NVFP4: 4 blocks of 36 B (4 UE4M3 scale bytes, 4 x 8 code bytes)
+template <>
+struct GemmFmt<PULSAR_QUANT_NVFP4> {
+    static constexpr uint32_t kSb = 144, kChunks = 9, kDSlot = 0;
+    static constexpr bool kBsums = false;
+};
 
 // bsums b[2t] + b[2t + 1] for t = 4 (kq & 1) + [0, 4) of a token, split as
 // 128 h + l: l bytes (kq < 2) or h bytes (kq >= 2)
@@ -273,6 +279,49 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[n][r] += xd * yd[r] * (float)isum[n][r];
                 }
+            } else if constexpr (Q == PULSAR_QUANT_NVFP4) {
+                // step t: block t / 2, 16-value sub-blocks s0 = 2 (t & 1) and
+                // s0 + 1; lane group kq holds sub-block s0 + kq / 2, values
+                // 8 (kq & 1) + [0, 8) (low / high nibbles of its 8 code bytes).
+                // Two MFMAs split the step's sum by sub-block (all 32 values,
+                // then the first sub-block alone); per sub-block the
+                // reference's sumf += (ue4m3 / 2) * sumi in order
+                // (pulsar_kernels.cu:5743-5771), then yd * sumf
+                float f[NT][4];
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) f[n][r] = 0.0f;
+                const uint32_t nsh = 4u * (kq & 1u);
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const uint8_t *bp = wrow + 36u * (uint32_t)(t >> 1);
+                    const uint8_t *sp = bp + 4u + 8u * (2u * (uint32_t)(t & 1) + (kq >> 1));
+                    const uint2 c = make_uint2(mxfp4_kv4(*(const uint32_t *)sp >> nsh),
+                                               mxfp4_kv4(*(const uint32_t *)(sp + 4) >> nsh));
+                    const uint2 c_lo = kq < 2 ? c : make_uint2(0u, 0u);
+                    const uint32_t e4 = *(const uint32_t *)bp;
+                    const float d0 = ue4m3f(byte_of(e4, 2u * (uint32_t)(t & 1))) * 0.5f;
+                    const float d1 = ue4m3f(byte_of(e4, 2u * (uint32_t)(t & 1) + 1u)) * 0.5f;
+#pragma unroll
+                    for (uint32_t n = 0; n < NT; n++) {
+                        const uint2 a = lds64(abase + 16u * n * kActPitch + 32u * t);
+                        const v4i d_all = mfma16x16x32(a, c);
+                        const v4i d_lo = mfma16x16x32(a, c_lo);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            f[n][r] += d0 * (float)d_lo[r];
+                            f[n][r] += d1 * (float)(d_all[r] - d_lo[r]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (uint32_t n = 0; n < NT; n++) {
+                    const float4 yd4 = lds_f4(yl + sbw * TOK + 16u * n + 4u * kq);
+                    const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[n][r] += yd[r] * f[n][r];
+                }
             } else {
                 const MmaQ4K::W wv = MmaQ4K::load_lds(wrow, kq);
                 int32_t isum[NT][4];
@@ -373,7 +422,8 @@ static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *
     return launch_ok("matmul_kq gemm launch");
 }
 
-// MFMA GEMM for token chunks / prefill (Q4_K, Q6_K); -1 for other formats.
+// MFMA GEMM for token chunks / prefill (the reference's prefill GEMM formats,
+// pulsar_kernels.cu:4914-4916: Q4_K, Q6_K, NVFP4); -1 for other formats.
 int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
                 uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
     const uint32_t nb = in_dim / 256u;
@@ -381,6 +431,7 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
     switch (quant) {
     case PULSAR_QUANT_Q6_K: return launch_gemm_q<PULSAR_QUANT_Q6_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
     case PULSAR_QUANT_Q4_K: return launch_gemm_q<PULSAR_QUANT_Q4_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
+    case PULSAR_QUANT_NVFP4: return launch_gemm_q<PULSAR_QUANT_NVFP4>(out, w, xq, nb, out_dim, n_tok, row_bytes);
     default: return -1;
     }
 }
