@@ -17,6 +17,8 @@
 //   D[i][j]: lane j + 16 * (i / 4), element i % 4
 // Which 8 slots a lane group holds does not matter: A and B hold the same
 // ones, and every sum is over whole lane groups.
+#include <type_traits>
+
 #include "pk_rowdot.h"
 #include "pk_route.h"
 
@@ -110,6 +112,35 @@ struct MmaQ4K {
     }
 };
 
+// Q5_K (176 B: d, dmin, scales[12], qh[32] @16, qs[128] @48): Q4_K's codes
+// of lane group kq plus the fifth bit of value 32t + 8kq + i, bit t of qh
+// byte 8kq + i (pulsar_kernels.cu:5892-5918).
+struct MmaQ5K {
+    static constexpr uint32_t kSbBytes = 176;
+    struct W {
+        uint2 q[4];  // qs bytes 32c + 8kq + [0, 8)
+        uint4 hdr;   // d, dmin, scales[12]
+        uint2 qh;    // qh bytes 8kq + [0, 8)
+    };
+    PK_DEV static W load_lds(const uint8_t *blk, uint32_t kq) {
+        W w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) w.q[c] = lds64(blk + 48u + 32u * c + 8u * kq);
+        w.hdr = lds128(blk);
+        w.qh = lds64(blk + 16u + 8u * kq);
+        return w;
+    }
+    PK_DEV static uint2 codes(const W &w, int t) {
+        const uint2 q = w.q[t >> 1];
+        const uint32_t sh = 4u * (t & 1);
+        return make_uint2(((q.x >> sh) & 0x0f0f0f0fu) | (((w.qh.x >> t) & 0x01010101u) << 4),
+                          ((q.y >> sh) & 0x0f0f0f0fu) | (((w.qh.y >> t) & 0x01010101u) << 4));
+    }
+};
+// the scale/min K-quant decoders by format
+template <uint32_t Q>
+using MmaKq = typename std::conditional<Q == PULSAR_QUANT_Q5_K, MmaQ5K, MmaQ4K>::type;
+
 // Per-format pieces of the dense GEMM: super-block bytes, 16-byte copies
 // per row super-block (the last one may overlap the previous: it ends at
 // the super-block's end), the LDS slot offset of f16 d, bsums needed.
@@ -123,6 +154,11 @@ struct GemmFmt<PULSAR_QUANT_Q6_K> {
 template <>
 struct GemmFmt<PULSAR_QUANT_Q4_K> {
     static constexpr uint32_t kSb = 144, kChunks = 9, kDSlot = 0;
+    static constexpr bool kBsums = true;
+};
+template <>
+struct GemmFmt<PULSAR_QUANT_Q5_K> {
+    static constexpr uint32_t kSb = 176, kChunks = 11, kDSlot = 0;
     static constexpr bool kBsums = true;
 };
 // NVFP4: 4 blocks of 36 B (4 UE4M3 scale bytes, 4 x 8 code bytes)
@@ -322,8 +358,9 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[n][r] += yd[r] * f[n][r];
                 }
-            } else {
-                const MmaQ4K::W wv = MmaQ4K::load_lds(wrow, kq);
+            } else {  // Q4_K, Q5_K
+                using M = MmaKq<Q>;
+                const typename M::W wv = M::load_lds(wrow, kq);
                 int32_t isum[NT][4];
 #pragma unroll
                 for (uint32_t n = 0; n < NT; n++)
@@ -335,7 +372,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                     int32_t sc, mn;
                     Fmt<PULSAR_QUANT_Q4_K>::scale_min(wv.hdr, (uint32_t)t, sc, mn);
                     mins[t >> 2] |= (uint32_t)mn << (8 * (t & 3));
-                    const uint2 b = MmaQ4K::codes(wv, t);
+                    const uint2 b = M::codes(wv, t);
 #pragma unroll
                     for (uint32_t n = 0; n < NT; n++) {
                         const v4i d = mfma16x16x32(lds64(abase + 16u * n * kActPitch + 32u * t), b);
@@ -423,7 +460,8 @@ static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *
 }
 
 // MFMA GEMM for token chunks / prefill (the reference's prefill GEMM formats,
-// pulsar_kernels.cu:4914-4916: Q4_K, Q6_K, NVFP4); -1 for other formats.
+// pulsar_kernels.cu:4914-4916: Q4_K, Q6_K, NVFP4, plus Q5_K, which the
+// reference runs through its per-token matvec); -1 for other formats.
 int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t in_dim,
                 uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
     const uint32_t nb = in_dim / 256u;
@@ -432,6 +470,7 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
     case PULSAR_QUANT_Q6_K: return launch_gemm_q<PULSAR_QUANT_Q6_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
     case PULSAR_QUANT_Q4_K: return launch_gemm_q<PULSAR_QUANT_Q4_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
     case PULSAR_QUANT_NVFP4: return launch_gemm_q<PULSAR_QUANT_NVFP4>(out, w, xq, nb, out_dim, n_tok, row_bytes);
+    case PULSAR_QUANT_Q5_K: return launch_gemm_q<PULSAR_QUANT_Q5_K>(out, w, xq, nb, out_dim, n_tok, row_bytes);
     default: return -1;
     }
 }
@@ -513,6 +552,16 @@ struct GmmqFmt<PULSAR_QUANT_Q4_K> {
     PK_DEV static uint32_t tail_off(uint32_t, uint32_t, uint32_t) { return 0u; }
 };
 template <>
+struct GmmqFmt<PULSAR_QUANT_Q5_K> {
+    static constexpr uint32_t kPieces = 11, kTails = 0, kTailBytes = 4;  // the whole 176 bytes
+    static constexpr uint32_t kTailSlot = 0;
+    static constexpr uint32_t kSlot = 176;
+    PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
+        return (sb < lim ? sb : lim - 1u) * 176u + 16u * c;
+    }
+    PK_DEV static uint32_t tail_off(uint32_t, uint32_t, uint32_t) { return 0u; }
+};
+template <>
 struct GmmqFmt<PULSAR_QUANT_Q6_K> {
     static constexpr uint32_t kPieces = 13, kTails = 1, kTailBytes = 2;  // bytes 0..207, then d
     static constexpr uint32_t kTailSlot = 208;
@@ -566,7 +615,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
     constexpr bool kMx = Q == PULSAR_QUANT_MXFP4;
     // MXFP4, Q4_K and Q6_K super-block rows are 136-210 contiguous bytes already
-    constexpr uint32_t S = (kMx || Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q6_K) ? 1u : kGqSbs;
+    constexpr uint32_t S = (kMx || Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q5_K || Q == PULSAR_QUANT_Q6_K) ? 1u : kGqSbs;
     constexpr uint32_t kRowL = S * F::kSlot + 16u;        // LDS bytes per row (S slots, padded)
     constexpr uint32_t kWp = NM * 16u * S * F::kPieces;  // weight pieces per step
     constexpr uint32_t kWj = (kWp + 63u) / 64u;         // ... per lane
@@ -733,15 +782,16 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[mt][r] += xd * yd[r] * (float)isum[mt][r];
                 }
-            } else if constexpr (Q == PULSAR_QUANT_Q4_K) {
+            } else if constexpr (Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q5_K) {
                 // one MFMA per 32-value sub-block, its 6-bit scale on D; the
                 // min term from two MFMAs on the bsum pair sums split 128 h + l
-                MmaQ4K::W wv[NM];
+                using M = MmaKq<Q>;
+                typename M::W wv[NM];
                 int32_t isum[NM][4];
                 uint32_t mins[NM][2];
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    wv[mt] = MmaQ4K::load_lds(ws + mt * 16u * kRowL, kq);
+                    wv[mt] = M::load_lds(ws + mt * 16u * kRowL, kq);
                     mins[mt][0] = mins[mt][1] = 0u;
 #pragma unroll
                     for (int r = 0; r < 4; r++) isum[mt][r] = 0;
@@ -754,7 +804,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
                         int32_t sc, mn;
                         Fmt<PULSAR_QUANT_Q4_K>::scale_min(wv[mt].hdr, (uint32_t)t, sc, mn);
                         mins[mt][t >> 2] |= (uint32_t)mn << (8 * (t & 3));
-                        const v4i d = mfma16x16x32(a, MmaQ4K::codes(wv[mt], t));
+                        const v4i d = mfma16x16x32(a, M::codes(wv[mt], t));
 #pragma unroll
                         for (int r = 0; r < 4; r++) isum[mt][r] += __mul24(sc, d[r]);
                     }
@@ -911,7 +961,7 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
                           const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
                           uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
     if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS && quant != PULSAR_QUANT_MXFP4 &&
-        quant != PULSAR_QUANT_Q4_K && quant != PULSAR_QUANT_Q6_K)
+        quant != PULSAR_QUANT_Q4_K && quant != PULSAR_QUANT_Q5_K && quant != PULSAR_QUANT_Q6_K)
         return -1;
     const uint32_t k_blocks = (k_dim + 255u) / 256u;
     const uint32_t lim = quant == PULSAR_QUANT_MXFP4 ? k_dim / 32u : k_blocks;
@@ -940,6 +990,10 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
         PK_GQ(PULSAR_QUANT_Q4_K, true);
     else if (quant == PULSAR_QUANT_Q4_K)
         PK_GQ(PULSAR_QUANT_Q4_K, false);
+    else if (quant == PULSAR_QUANT_Q5_K && pair)
+        PK_GQ(PULSAR_QUANT_Q5_K, true);
+    else if (quant == PULSAR_QUANT_Q5_K)
+        PK_GQ(PULSAR_QUANT_Q5_K, false);
     else if (quant == PULSAR_QUANT_Q6_K && pair)
         PK_GQ(PULSAR_QUANT_Q6_K, true);
     else if (quant == PULSAR_QUANT_Q6_K)

@@ -170,7 +170,7 @@ def test_pair_down_decode_shapes(dev):
 @pytest.mark.parametrize("gq,dq,n_tok", [(QUANT_Q2_K, QUANT_Q2_K, 16), (QUANT_IQ2_XXS, QUANT_IQ2_XXS, 16),
                                           (QUANT_Q2_K, QUANT_Q2_K, 40), (QUANT_IQ2_XXS, QUANT_IQ2_XXS, 40),
                                           (QUANT_Q4_K, QUANT_Q6_K, 16), (QUANT_Q4_K, QUANT_Q6_K, 40),
-                                          (QUANT_Q6_K, QUANT_Q4_K, 24)])
+                                          (QUANT_Q6_K, QUANT_Q4_K, 24), (fm.QUANT_Q5_K, fm.QUANT_Q5_K, 40)])
 def test_grouped_mfma_kquants(dev, gq, dq, n_tok):
     """K-quant / IQ2_XXS groups run on the matrix cores: pair and down
     against the oracle (more than 16 pairs per group at n_tok 40: several
@@ -205,7 +205,7 @@ def test_grouped_mfma_kquants(dev, gq, dq, n_tok):
     assert np.array_equal(down(out), acc)
 
 
-@pytest.mark.parametrize("gq", [QUANT_Q2_K, QUANT_IQ2_XXS, QUANT_Q4_K, QUANT_Q6_K])
+@pytest.mark.parametrize("gq", [QUANT_Q2_K, QUANT_IQ2_XXS, QUANT_Q4_K, QUANT_Q6_K, fm.QUANT_Q5_K])
 def test_grouped_mfma_pair_row_tail(dev, gq):
     """A pair stage whose row count (200) is not a multiple of the 16-row
     tile, and 3 super-blocks (768) over the 4 waves' ranges."""
@@ -448,7 +448,8 @@ def test_pair_down_every_format(dev, q):
 
 @pytest.mark.parametrize("q", NEW_FORMATS, ids=lambda q: fm.NAMES[q])
 def test_grouped_every_format(dev, q):
-    """The same formats through the grouped entry points (lane kernels)."""
+    """The same formats through the grouped entry points (Q5_K on the matrix
+    cores, the rest on the lane kernels)."""
     L = Layer(q, q, hidden=512, ffn=256, E=5, n_used=4, n_tok=12, null_slots=(7,))
     hptrs, dptrs = L.ptrs()
     xq = oracle.quantize_q8_k(L.x)
