@@ -581,7 +581,7 @@ constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy 
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
 #ifndef PK_GQ_ACT_LDS_MX
-#define PK_GQ_ACT_LDS_MX 40960u
+#define PK_GQ_ACT_LDS_MX 61440u
 #endif
 constexpr uint32_t kGqActLdsMx = PK_GQ_ACT_LDS_MX;  // the same for MXFP4 experts
 
@@ -604,8 +604,15 @@ PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
     return __builtin_amdgcn_perm(y, x, 0x06040200u);  // bytes 0, 2 of x, then of y
 }
 
+// Waves per block, 16 rows each. MXFP4 blocks take 8: their pair tiles are
+// large (16 pairs of 2880-value rows, ~58 KiB), and sharing one tile over
+// 128 rows keeps twice the waves per CU resident (c5 64-token layer 215 ->
+// 203 us); the K-quant layers measured slower with 8 (c4 Q2_K 183 -> 192 us).
+template <uint32_t Q>
+constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 8u : 4u;
+
 template <uint32_t Q, bool PAIR>
-__global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
+__global__ __launch_bounds__(64 * kGqWaves<Q>) void moe_grouped_mmq_kq_kernel(
         float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
         const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
         const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t lim, uint32_t n_rows,
@@ -624,7 +631,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     constexpr uint32_t kTjA = kTj > 0u ? kTj : 1u;  // array extent
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint2 lut[kIq2 ? kIq2LutRows : 1];
-    __shared__ __align__(16) uint8_t wl[4][NM * 16u * kRowL];  // [wave][matrix][row][step slot]
+    __shared__ __align__(16) uint8_t wl[kGqWaves<Q>][NM * 16u * kRowL];  // [wave][matrix][row][step slot]
     __shared__ uint32_t pr_l[kGqPairs];
     if (kIq2) {
         fill_iq2xxs_lut(lut);
@@ -639,7 +646,7 @@ __global__ __launch_bounds__(256) void moe_grouped_mmq_kq_kernel(
     if (s0 >= s1) return;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
-    const uint32_t rw0 = blockIdx.x * 64u + wave * 16u;  // the wave's first row
+    const uint32_t rw0 = (blockIdx.x * kGqWaves<Q> + wave) * 16u;  // the wave's first row
     const bool active = rw0 < n_rows;                    // wave-uniform
     const uint32_t n_steps = (k_blocks + S - 1u) / S;
     auto row_src = [&](uint32_t mt, uint32_t r) {
@@ -973,9 +980,10 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
     uint32_t pmax = budget / per_pair;
     pmax = pmax < kGqPairs ? pmax : kGqPairs;
     const size_t lds = (size_t)pmax * per_pair;
-    const dim3 grid((n_rows + 63u) / 64u, n_group);
 #define PK_GQ(Q, P)                                                                                              \
-    hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P>), grid, dim3(256), lds, pk::stream(), out,             \
+    hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P>),                                                        \
+                       dim3((n_rows + 16u * kGqWaves<Q> - 1u) / (16u * kGqWaves<Q>), n_group),                     \
+                       dim3(64u * kGqWaves<Q>), lds, pk::stream(), out,                                           \
                        (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs, weights, \
                        act, k_blocks, lim, n_rows, n_used, row_bytes, act_op, pmax)
     if (quant == PULSAR_QUANT_Q2_K && pair)
