@@ -170,36 +170,132 @@ __global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_pt
             [&](uint32_t i) { return ptrs[i]; }, n, n_used, max_groups);
 }
 
-// router_select (modes 0/1) + route_ptrs + group_csr in one block: the 16
-// waves route tokens (wave w takes tokens w, w + 16, ...; the arithmetic of
-// route_lane, as the fused pair kernel routes), keeping every pair's
-// expert in LDS, then the CSR is built from those as group_csr_kernel does.
+// Maximum over the lpt-lane group holding this lane (lpt a power of two,
+// 4..64), in every lane of the group: butterfly steps quad_perm 1032 and
+// 2301, row_half_mirror (8), row_mirror (16), a swizzle lane ^ 16 (32) and a
+// permute lane ^ 32 (64).
+PK_DEV uint32_t group_max_u32(uint32_t v, uint32_t lpt) {
+    auto mx = [](int32_t a, int32_t b) { return (uint32_t)a > (uint32_t)b ? a : b; };
+    int32_t x = (int32_t)v;
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    if (lpt >= 8u) x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false));
+    if (lpt >= 16u) x = mx(x, __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false));
+    if (lpt >= 32u) x = mx(x, __builtin_amdgcn_ds_swizzle(x, 0x401F));
+    if (lpt >= 64u) x = mx(x, __shfl_xor(x, 32, 64));
+    return (uint32_t)x;
+}
+
+// router_select (modes 0/1) + route_ptrs + group_csr in one block. A wave
+// routes 64 / lpt tokens at once, lpt lanes per token (lane kk of a group
+// holds experts kk J .. kk J + J - 1): every top-k round is a group
+// maximum, the winner is the group's lowest lane holding it (its lowest
+// such expert), which records (expert, prob) for round k in LDS and drops
+// that score to -inf, as topk_wave does for one token per wave. The router
+// weights then follow route_lane's arithmetic from the recorded winners in
+// round order. Every pair's expert is kept in LDS and the CSR is built from
+// those as group_csr_kernel does.
 template <uint32_t J>
 __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
         int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
         float *__restrict__ slot_w, pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
         uint32_t *__restrict__ pairs, const float *__restrict__ logits, const float *__restrict__ rbias,
         uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode, pulsar_expert_bank bank,
-        SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups) {
+        SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups, uint32_t lpt) {
     __shared__ int32_t eid_l[kMaxCsrPairs];  // routed expert, or -2 - s for shared slot s
+    __shared__ int32_t win_e[kMaxCsrPairs];  // token t's round-k winner at t k_used + k
+    __shared__ float win_p[kMaxCsrPairs];    // ... and its prob
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n_slots = k_used + n_shared;
-    for (uint32_t t = wave; t < n_tok; t += kCsrThreads / 64u) {
-        int32_t e;
+    const uint32_t tpw = 64u / lpt, g0 = lane & ~(lpt - 1u), kk = lane - g0;
+    const uint64_t gmask = lpt == 64u ? ~0ull : (1ull << lpt) - 1ull;
+    const uint32_t kNegInf = score_key(-INFINITY);
+    for (uint32_t tb = wave * tpw; tb < n_tok; tb += (kCsrThreads / 64u) * tpw) {
+        const uint32_t t = tb + lane / lpt;
+        const bool t_ok = t < n_tok;
+        const float *lg = logits + (uint64_t)(t_ok ? t : n_tok - 1u) * n_expert;
+        const float *bsrc = rbias ? rbias : lg;
+        float raw_l[J], bias_l[J];
+#pragma unroll
+        for (uint32_t j = 0; j < J; j++) {  // every load before any use, clamped indices
+            const uint32_t e = kk * J + j, ec = e < n_expert ? e : n_expert - 1u;
+            raw_l[j] = lg[ec];
+            bias_l[j] = bsrc[ec];
+        }
+        uint32_t key[J];
+        float prob[J];
+#pragma unroll
+        for (uint32_t j = 0; j < J; j++) {
+            const float p = mode == 1u ? raw_l[j] : router_sigmoid(raw_l[j]);
+            prob[j] = p;
+            key[j] = kk * J + j < n_expert ? score_key(p + (rbias ? bias_l[j] : 0.0f)) : 0u;
+        }
+        // this lane's best: first (lowest index) maximal key
+        uint32_t bk = 0u, bj = 0u;
+        float bp = 0.0f;
+        auto lane_best = [&]() {
+            bk = 0u;
+            bj = 0u;
+            bp = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < J; j++)
+                if (key[j] > bk) {
+                    bk = key[j];
+                    bj = j;
+                    bp = prob[j];
+                }
+        };
+        lane_best();
+        for (uint32_t k = 0; k < k_used; k++) {
+            const uint32_t m = group_max_u32(bk, lpt);  // 0: no candidate left (all NaN)
+            const uint64_t gm = (__ballot(m != 0u && bk == m) >> g0) & gmask;
+            const bool mine = gm != 0ull && kk == (uint32_t)__builtin_ctzll(gm);
+            if (t_ok && (mine || (m == 0u && kk == 0u))) {
+                win_e[t * k_used + k] = mine ? (int32_t)(kk * J + bj) : -1;
+                win_p[t * k_used + k] = mine ? bp : 0.0f;
+            }
+            if (mine) {
+#pragma unroll
+                for (uint32_t j = 0; j < J; j++)
+                    if (j == bj) key[j] = kNegInf;
+                lane_best();
+            }
+        }
+        // the winners' LDS records visible to the wave's other lanes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (!t_ok) continue;
+        // route_lane's weights: sequential sum and max of the winners' probs
+        float sum = 0.0f, wmax = -INFINITY;
+        for (uint32_t k = 0; k < k_used; k++) {
+            const float p = win_p[t * k_used + k];
+            sum += p;
+            wmax = fmaxf(wmax, p);
+        }
+        const uint32_t ks = kk < k_used ? kk : 0u;
+        const int32_t e = win_e[t * k_used + ks];
+        const float pk = win_p[t * k_used + ks];
         float w;
-        route_lane<J>(logits + (uint64_t)t * n_expert, rbias, n_expert, k_used, scale, mode, e, w);
-        if (lane < k_used) {
-            const uint64_t i = (uint64_t)t * n_slots + lane;
-            sel[(uint64_t)t * k_used + lane] = e;
-            rw[(uint64_t)t * k_used + lane] = w;
+        if (mode == 1u) {
+            float es = 0.0f;
+            for (uint32_t k = 0; k < k_used; k++) es += expf(win_p[t * k_used + k] - wmax);
+            w = expf(pk - wmax) / es * scale;
+        } else {
+            w = pk / fmaxf(sum, 6.103515625e-5f) * scale;
+        }
+        if (kk < k_used) {
+            const uint64_t i = (uint64_t)t * n_slots + kk;
+            sel[(uint64_t)t * k_used + kk] = e;
+            rw[(uint64_t)t * k_used + kk] = w;
             ptrs[i] = bank_ptrs(bank, n_expert, e);
             slot_w[i] = w;
             eid_l[i] = e < 0 ? -1 : e;
-        } else if (lane < n_slots) {
-            const uint64_t i = (uint64_t)t * n_slots + lane;
-            ptrs[i] = shared.p[lane - k_used];
+        } else if (kk < n_slots) {
+            const uint64_t i = (uint64_t)t * n_slots + kk;
+            ptrs[i] = shared.p[kk - k_used];
             slot_w[i] = 1.0f;
-            eid_l[i] = -2 - (int32_t)(lane - k_used);
+            eid_l[i] = -2 - (int32_t)(kk - k_used);
         }
     }
     __syncthreads();
@@ -254,12 +350,18 @@ extern "C" int pulsar_moe_route_group(void *selected, void *weights, void *ptrs,
         return pk::reject("moe route group");
     pk::SharedSlots sh = {};
     for (uint32_t s = 0; s < n_shared; s++) sh.p[s] = shared[s];
+    // lanes per token: a power of two holding the token's experts (J per
+    // lane) and its slots, at least 4
+    const uint32_t jl = n_expert <= 256u ? 4u : n_expert <= 512u ? 8u : 16u;
+    const uint32_t need = (n_expert + jl - 1u) / jl > n_slots ? (n_expert + jl - 1u) / jl : n_slots;
+    uint32_t lpt = 4u;
+    while (lpt < need) lpt <<= 1;
 #define PK_RG(J)                                                                                                 \
     hipLaunchKernelGGL(pk::route_group_kernel<J>, dim3(1), dim3(pk::kCsrThreads), 0, pk::stream(),              \
                        (int32_t *)selected, (float *)weights, (pulsar_expert_ptrs *)ptrs, (float *)slot_weights, \
                        (pulsar_expert_ptrs *)gptrs, (uint32_t *)starts, (uint32_t *)pairs, (const float *)logits, \
                        (const float *)router_bias, n_expert, k_used, weight_scale, softmax_mode, *bank, sh, n_shared, \
-                       n_tok, max_groups)
+                       n_tok, max_groups, lpt)
     if (n_expert <= 256u)
         PK_RG(4);
     else if (n_expert <= 512u)
