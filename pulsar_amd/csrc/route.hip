@@ -40,12 +40,16 @@ constexpr uint32_t kHashSlots = 4096;    // open-addressing table, >= 2 x kMaxCs
 PK_DEV uint32_t block_scan2(uint32_t v0, uint32_t v1, uint32_t &e0, uint32_t &e1, uint32_t *wsum) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t own = v0 + v1;
-    uint32_t s = own;
-#pragma unroll
-    for (uint32_t d = 1; d < 64u; d <<= 1) {
-        const uint32_t o = __shfl_up(s, d, 64);
-        if (lane >= d) s += o;
-    }
+    // inclusive wave scan by DPP: row_shr 1/2/4/8 within 16-lane rows (lanes
+    // without a source add 0), then row_bcast 15 / 31 carry the row totals
+    int32_t x = (int32_t)own;
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+    const uint32_t s = (uint32_t)x;
     if (lane == 63u) wsum[wave] = s;
     __syncthreads();
     uint32_t base = 0, total = 0;
@@ -267,11 +271,17 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (!t_ok) continue;
         // route_lane's weights: sequential sum and max of the winners' probs
+        // (all the token's records read at once, clamped to its k_used;
+        // k_used <= 16, a CSR slot limit)
+        float wp[16];
+#pragma unroll
+        for (uint32_t k = 0; k < 16u; k++) wp[k] = win_p[t * k_used + (k < k_used ? k : k_used - 1u)];
         float sum = 0.0f, wmax = -INFINITY;
-        for (uint32_t k = 0; k < k_used; k++) {
-            const float p = win_p[t * k_used + k];
-            sum += p;
-            wmax = fmaxf(wmax, p);
+#pragma unroll
+        for (uint32_t k = 0; k < 16u; k++) {
+            if (k >= k_used) break;  // wave-uniform
+            sum += wp[k];
+            wmax = fmaxf(wmax, wp[k]);
         }
         const uint32_t ks = kk < k_used ? kk : 0u;
         const int32_t e = win_e[t * k_used + ks];
@@ -279,7 +289,11 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
         float w;
         if (mode == 1u) {
             float es = 0.0f;
-            for (uint32_t k = 0; k < k_used; k++) es += expf(win_p[t * k_used + k] - wmax);
+#pragma unroll
+            for (uint32_t k = 0; k < 16u; k++) {
+                if (k >= k_used) break;
+                es += expf(wp[k] - wmax);
+            }
             w = expf(pk - wmax) / es * scale;
         } else {
             w = pk / fmaxf(sum, 6.103515625e-5f) * scale;
