@@ -106,29 +106,25 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
     lane_best();
     sum = 0.0f;
     wmax = -INFINITY;
+    // A round has no divergent section: the winner's update and the record
+    // of winner k are selects on every lane (a round is one dependent chain,
+    // and exec-mask branches lengthen it)
     for (uint32_t k = 0; k < k_used; k++) {
-        const uint32_t m = wave_max_u32(bk);
-        int32_t w_e = -1;  // no candidate: every routed score is NaN
-        float w_p = 0.0f;
-        if (m != 0u) {
-            const uint64_t bal = __ballot(bk == m);
-            const int f = __builtin_ctzll(bal);
-            w_e = __builtin_amdgcn_readlane((int)(lane * J + bj), f);
-            w_p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bp), f));
-            if ((int)lane == f) {
+        const uint32_t m = wave_max_u32(bk);  // 0: no candidate, every routed score is NaN
+        const int f = __builtin_ctzll(__ballot(bk == m));
+        const int32_t e_f = __builtin_amdgcn_readlane((int)(lane * J + bj), f);
+        const float p_f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bp), f));
+        const int32_t w_e = m != 0u ? e_f : -1;
+        const float w_p = m != 0u ? p_f : 0.0f;
+        const bool mine = m != 0u && (int)lane == f;
 #pragma unroll
-                for (uint32_t j = 0; j < J; j++)
-                    if (j == bj) key[j] = kNegInf;
-                lane_best();
-            }
-        }
-        if (lane == (k & 63u)) {
+        for (uint32_t j = 0; j < J; j++) key[j] = mine && j == bj ? kNegInf : key[j];
+        lane_best();
+        const bool rec = lane == (k & 63u);
 #pragma unroll
-            for (uint32_t j = 0; j < J; j++)
-                if (j == (k >> 6)) {
-                    win[j] = w_e;
-                    wprob[j] = w_p;
-                }
+        for (uint32_t j = 0; j < J; j++) {
+            win[j] = rec && j == (k >> 6) ? w_e : win[j];
+            wprob[j] = rec && j == (k >> 6) ? w_p : wprob[j];
         }
         sum += w_p;
         wmax = fmaxf(wmax, w_p);

@@ -207,8 +207,8 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
         uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode, pulsar_expert_bank bank,
         SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups, uint32_t lpt) {
     __shared__ int32_t eid_l[kMaxCsrPairs];  // routed expert, or -2 - s for shared slot s
-    __shared__ int32_t win_e[kMaxCsrPairs];  // token t's round-k winner at t k_used + k
-    __shared__ float win_p[kMaxCsrPairs];    // ... and its prob
+    __shared__ int32_t win_e[kMaxCsrPairs + 64];  // token t's round-k winner at t k_used + k (+ spare slots)
+    __shared__ float win_p[kMaxCsrPairs + 64];    // ... and its prob
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t n_slots = k_used + n_shared;
     const uint32_t tpw = 64u / lpt, g0 = lane & ~(lpt - 1u), kk = lane - g0;
@@ -250,20 +250,19 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
                 }
         };
         lane_best();
+        // no divergent section in a round: lanes that record nothing store
+        // to their own spare slot, and the winner's update is a select
         for (uint32_t k = 0; k < k_used; k++) {
             const uint32_t m = group_max_u32(bk, lpt);  // 0: no candidate left (all NaN)
             const uint64_t gm = (__ballot(m != 0u && bk == m) >> g0) & gmask;
             const bool mine = gm != 0ull && kk == (uint32_t)__builtin_ctzll(gm);
-            if (t_ok && (mine || (m == 0u && kk == 0u))) {
-                win_e[t * k_used + k] = mine ? (int32_t)(kk * J + bj) : -1;
-                win_p[t * k_used + k] = mine ? bp : 0.0f;
-            }
-            if (mine) {
+            const bool rec = t_ok && (mine || (m == 0u && kk == 0u));
+            const uint32_t at = rec ? t * k_used + k : kMaxCsrPairs + lane;
+            win_e[at] = mine ? (int32_t)(kk * J + bj) : -1;
+            win_p[at] = mine ? bp : 0.0f;
 #pragma unroll
-                for (uint32_t j = 0; j < J; j++)
-                    if (j == bj) key[j] = kNegInf;
-                lane_best();
-            }
+            for (uint32_t j = 0; j < J; j++) key[j] = mine && j == bj ? kNegInf : key[j];
+            lane_best();
         }
         // the winners' LDS records visible to the wave's other lanes
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
