@@ -153,6 +153,24 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
     const uint32_t token = blockIdx.y, wave = threadIdx.x / 64u, nw = blockDim.x / 64u;
     const uint32_t n_blk = n_used * mid_blocks;
     float *part = (float *)(acts_lds + n_blk * kActLdsPitch);  // [n_pass][n_used][16]
+    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
+    const uint32_t rpp = 64u >> lpr_log2;
+    const uint32_t pass0 = blockIdx.x * n_pass;
+    // Unstaged rows: the wave's first (pass, slot) item has its weights
+    // requested before the mid rows are loaded and quantized, so their HBM
+    // latency overlaps that work. A NULL expert reads the token's mid row
+    // instead (in bounds: a weight row is shorter than 4 bytes per value)
+    // and is not used.
+    typename Fmt<Q>::W w_first[UPLMAX];
+    if constexpr (NPL == 0) {
+        const uint32_t ks = wave < n_pass * n_used ? wave : 0u;
+        const uint32_t k = ks / n_used, s = ks - k * n_used;
+        const uint32_t row = (pass0 + k) * rpp + rg.rip;
+        const uint8_t *dp = (const uint8_t *)ptrs[(uint64_t)token * n_used + s].down;
+        const uint8_t *src = dp ? dp + (uint64_t)(row < out_dim ? row : 0u) * row_bytes
+                                : (const uint8_t *)(mid + (uint64_t)token * n_used * mid_dim);
+        load_row_w<Q, UPLMAX>(as_global(src), rg, w_first);
+    }
     // the wave's mid blocks blk = wave + nw i, loaded four at a time before use
     for (uint32_t base = wave; base < n_blk; base += 4u * nw) {
         float v[4][4];
@@ -175,10 +193,7 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
         w_l[s] = slot_w ? slot_w[(uint64_t)token * n_used + s] : 0.0f;
     }
     __syncthreads();
-    const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
-    const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t act_bytes = mid_blocks * kActLdsPitch;
-    const uint32_t pass0 = blockIdx.x * n_pass;
     for (uint32_t ks = wave; ks < n_pass * n_used; ks += nw) {
         const uint32_t k = ks / n_used, s = ks - k * n_used;
         const uint32_t row = (pass0 + k) * rpp + rg.rip;
@@ -187,8 +202,13 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
         float v = -0.0f;
         if (p_l[s].down) {
             typename Fmt<Q>::W w[UPLMAX];
-            load_one_row<Q, UPLMAX, NPL, kFusedDownWaves>(
-                as_global(p_l[s].down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
+            if (NPL == 0 && ks == wave) {
+#pragma unroll
+                for (uint32_t u = 0; u < UPLMAX; u++) w[u] = w_first[u];
+            } else {
+                load_one_row<Q, UPLMAX, NPL, kFusedDownWaves>(
+                        as_global(p_l[s].down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
+            }
             Act a[UPLMAX];
             load_row_acts_lds<Q, UPLMAX>(acts_lds + s * act_bytes, rg, a);
             v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
