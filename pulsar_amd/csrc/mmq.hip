@@ -831,14 +831,19 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) void moe_grouped_mmq_kq_kernel(
                     }
                 }
             } else if constexpr (!kIq2) {
-                uint4 sc[NM];
+                uint4 sc[NM], scl[NM];
                 uint2 qv[NM][2];
                 v4i isum[NM];
-                const uint32_t hsh = 8u * (kq >> 1);
+                // v_perm selectors: scale byte 2 (t & 1) + kq / 2 of scale word
+                // t / 2 into bytes 0 and 2, zeros into bytes 1 and 3
+                const uint32_t sel_even = 0x0C000C00u + (kq >> 1) * 0x00010001u, sel_odd = sel_even + 0x00020002u;
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
                     const uint8_t *wm = ws + mt * 16u * kRowL;
                     sc[mt] = *(const uint4 *)wm;
+                    // the 4-bit scales (low nibbles), masked once per super-block
+                    scl[mt] = make_uint4(sc[mt].x & 0x0f0f0f0fu, sc[mt].y & 0x0f0f0f0fu, sc[mt].z & 0x0f0f0f0fu,
+                                         sc[mt].w & 0x0f0f0f0fu);
 #pragma unroll
                     for (uint32_t k = 0; k < 2; k++)
                         qv[mt][k] = *(const uint2 *)(wm + 16u + 32u * k + 16u * (kq >> 1) + 8u * (kq & 1u));
@@ -853,9 +858,8 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) void moe_grouped_mmq_kq_kernel(
                         // scales of sub-blocks 2t + kq / 2 (t even: byte kq / 2 of
                         // scale word t / 2, t odd: byte kq / 2 + 2), as both
                         // 16-bit halves of s2
-                        const uint32_t scw[4] = {sc[mt].x, sc[mt].y, sc[mt].z, sc[mt].w};
-                        const uint32_t pr2 = (scw[t >> 1] >> hsh) & 0x000f000fu;
-                        const uint32_t s2 = __builtin_amdgcn_perm(0u, pr2, (t & 1u) ? 0x0C020C02u : 0x0C000C00u);
+                        const uint32_t scw[4] = {scl[mt].x, scl[mt].y, scl[mt].z, scl[mt].w};
+                        const uint32_t s2 = __builtin_amdgcn_perm(0u, scw[t >> 1], (t & 1u) ? sel_odd : sel_even);
                         // codes (0..3 per byte) times the scale, per 16-bit half:
                         // c0 sc + 256 c1 sc with c sc <= 45, so no carry between bytes
                         const uint2 q = qv[mt][t >> 2];
