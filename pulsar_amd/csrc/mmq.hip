@@ -611,8 +611,12 @@ PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
 template <uint32_t Q>
 constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 8u : 4u;
 
+// amdgpu_waves_per_eu(2): register allocation for at least two waves per
+// SIMD. Left to itself the compiler spends more (Q2_K pair 164 VGPRs, Q4_K
+// 240, Q5_K 286); with the bound, 152 / 161 / 231, no spills, and the c4
+// layers run 2-4% faster (Q2_K 182 -> 178 us, IQ2_XXS 205 -> 198 us).
 template <uint32_t Q, bool PAIR>
-__global__ __launch_bounds__(64 * kGqWaves<Q>) void moe_grouped_mmq_kq_kernel(
+__global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_eu(2))) void moe_grouped_mmq_kq_kernel(
         float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
         const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
         const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t lim, uint32_t n_rows,
