@@ -130,11 +130,13 @@ def test_fused_error_contract(dev):
 
 @pytest.mark.parametrize("E,k,n_tok,n_sh,mode,select_bias",
                          [(128, 8, 16, 0, 1, False), (32, 4, 64, 0, 1, True), (256, 8, 3, 1, 1, False),
-                          (300, 6, 40, 2, 0, True), (12, 3, 200, 0, 1, False)])
+                          (300, 6, 40, 2, 0, True), (12, 3, 200, 0, 1, False), (64, 6, 33, 1, 0, True),
+                          (20, 5, 70, 0, 1, False)])
 def test_route_group_matches_separate_calls(dev, E, k, n_tok, n_sh, mode, select_bias):
     """router_select + moe_route_ptrs + moe_group_csr against the fused
     launch: every output bit-identical (ties, an all-NaN token, shared
-    slots, a selection bias)."""
+    slots, a selection bias). The expert counts give lane groups of 4, 8,
+    16, 32 and 64 lanes per token."""
     hidden = ffn = 256
     L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=hidden, ffn=ffn, E=E + n_sh, n_used=k, n_tok=1)
     bank = _bank(L)
