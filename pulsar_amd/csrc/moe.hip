@@ -69,18 +69,24 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                                                        uint64_t row_bytes, const float *__restrict__ weights) {
     PK_FMT_LUT(Q)
     __shared__ float part[kSlotChunk][16];
+    __shared__ float bpart[BIAS ? kSlotChunk : 1][16];
     const uint32_t token = blockIdx.y;
     const uint32_t wave = threadIdx.x / 64u;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t row = blockIdx.x * rpp + rg.rip;
     const bool row_ok = row < out_dim;
-    float total = 0.0f;
+    float total = 0.0f, b = 0.0f;
     for (uint32_t base = 0; base < n_used; base += kSlotChunk) {
         const uint32_t end = base + kSlotChunk < n_used ? base + kSlotChunk : n_used;
         for (uint32_t s = base + wave; s < end; s += kWaves) {
             const uint64_t so = (uint64_t)token * n_used + s;
             const pulsar_expert_ptrs p = ptrs[so];
+            // the slot's bias term w_s down_b_s[row], requested with the
+            // slot's weights (a NULL bias adds +0, which leaves the bias sum,
+            // never -0, as skipping it would)
+            float bt = 0.0f;
+            if (BIAS && p.down_b) bt = weights[so] * ldwf(p.down_b + (row_ok ? row : 0u));
             // -0.0 is the additive identity for every float, so a skipped
             // slot (NULL down, pulsar_kernels.cu:2635) leaves the sum as is
             float v = -0.0f;
@@ -91,23 +97,21 @@ __global__ __launch_bounds__(256) void moe_down_kernel(float *__restrict__ out,
                 load_one_row<Q, UPLMAX, NPL>(as_global(p.down) + (uint64_t)(row_ok ? row : 0u) * row_bytes, rg, w);
                 v = row_finish(row_partial<Q, UPLMAX>(row_ok, rg, w, a, lut), rg);
             }
-            if (rg.holds_row()) part[s - base][rg.rip] = v;
+            if (rg.holds_row()) {
+                part[s - base][rg.rip] = v;
+                if (BIAS) bpart[s - base][rg.rip] = bt;
+            }
         }
         __syncthreads();
         if (wave == 0 && rg.holds_row())
-            for (uint32_t s = base; s < end; s++) total += part[s - base][rg.rip];
+            for (uint32_t s = base; s < end; s++) {
+                total += part[s - base][rg.rip];
+                if (BIAS) b += bpart[s - base][rg.rip];  // slot order, as moe_down_bias sums
+            }
         __syncthreads();
     }
     if (wave == 0 && rg.holds_row() && row_ok) {
-        if constexpr (BIAS) {
-            float b = 0.0f;
-            for (uint32_t s = 0; s < n_used; s++) {
-                const uint64_t so = (uint64_t)token * n_used + s;
-                const float *db = ptrs[so].down_b;
-                if (db) b += weights[so] * ldwf(db + row);
-            }
-            if (b != 0.0f) total += b;
-        }
+        if (BIAS && b != 0.0f) total += b;
         out[(uint64_t)token * out_dim + row] = total;
     }
 }
