@@ -301,6 +301,32 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(float *__restrict__ out,
     out[gid] = acc;
 }
 
+// sum_s w_s down_b_s[row] over the token's slots in slot order, NULL biases
+// skipped (pulsar_kernels.cu:3601-3619). Slots are taken kB at a time with
+// every load of the batch issued first: the slot records, then the bias
+// values (a NULL bias reads a valid dummy address and is not added).
+constexpr uint32_t kBiasBatch = 8;
+PK_DEV float slot_bias_sum(const pulsar_expert_ptrs *__restrict__ ptrs, const float *__restrict__ weights,
+                           uint64_t token, uint32_t n_used, uint64_t row) {
+    float b = 0.0f;
+    for (uint32_t s0 = 0; s0 < n_used; s0 += kBiasBatch) {
+        const float *db[kBiasBatch];
+        float wv[kBiasBatch], bv[kBiasBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBiasBatch; j++) {
+            const uint64_t so = token * n_used + (s0 + j < n_used ? s0 + j : n_used - 1u);
+            db[j] = ptrs[so].down_b;
+            wv[j] = weights[so];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBiasBatch; j++) bv[j] = ldwf(db[j] ? db[j] + row : weights + token * n_used);
+#pragma unroll
+        for (uint32_t j = 0; j < kBiasBatch; j++)
+            if (s0 + j < n_used && db[j]) b += wv[j] * bv[j];
+    }
+    return b;
+}
+
 // slot_sum_kernel then down_bias_kernel in one pass: the same two sums in
 // the same order, so the result is bit-identical to the two launches.
 __global__ __launch_bounds__(256) void slot_sum_bias_kernel(float *__restrict__ out,
@@ -313,13 +339,16 @@ __global__ __launch_bounds__(256) void slot_sum_bias_kernel(float *__restrict__ 
     const uint64_t token = gid / out_dim;
     const uint64_t row = gid - token * out_dim;
     float acc = 0.0f;
-    for (uint32_t s = 0; s < n_used; s++) acc += partial[(token * n_used + s) * out_dim + row];
-    float b = 0.0f;
-    for (uint32_t s = 0; s < n_used; s++) {
-        const uint64_t so = token * n_used + s;
-        const float *db = ptrs[so].down_b;
-        if (db) b += weights[so] * ldwf(db + row);
+    for (uint32_t s0 = 0; s0 < n_used; s0 += kBiasBatch) {  // the partials of a batch loaded first
+        float pv[kBiasBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBiasBatch; j++)
+            pv[j] = partial[(token * n_used + (s0 + j < n_used ? s0 + j : n_used - 1u)) * out_dim + row];
+#pragma unroll
+        for (uint32_t j = 0; j < kBiasBatch; j++)
+            if (s0 + j < n_used) acc += pv[j];
     }
+    const float b = slot_bias_sum(ptrs, weights, token, n_used, row);
     if (b != 0.0f) acc += b;
     out[gid] = acc;
 }
@@ -334,12 +363,7 @@ __global__ __launch_bounds__(256) void down_bias_kernel(float *__restrict__ out,
     if (gid >= total) return;
     const uint64_t token = gid / out_dim;
     const uint64_t row = gid - token * out_dim;
-    float b = 0.0f;
-    for (uint32_t s = 0; s < n_used; s++) {
-        const uint64_t so = token * n_used + s;
-        const float *db = ptrs[so].down_b;
-        if (db) b += weights[so] * ldwf(db + row);
-    }
+    const float b = slot_bias_sum(ptrs, weights, token, n_used, row);
     if (b != 0.0f) out[gid] += b;
 }
 
