@@ -85,10 +85,15 @@ static void launch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K 
                           uint32_t n_tok, uint64_t row_bytes) {
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t n_pass = (out_dim + rpp - 1u) / rpp;
-    // waves capped at PK_MV_WAVES (a few per SIMD on 256 CUs); larger
-    // matrices loop
+    // up to 4096 chunks one wave each; larger matrices loop over a wave
+    // count measured per format on 8192-32768-row matrices: Q6_K (the
+    // heaviest decode per byte) runs best on 3072 waves, 3 blocks per CU
+    // (8192 x 4096: 7.6 -> 7.2 us; 16384 x 4096: 13.0 -> 11.8 us), Q4_K and
+    // Q2_K on 6144 (Q4_K 12288 x 4096: 7.9 -> 7.4 us; Q2_K 16384 x 4096:
+    // 7.6 -> 7.2 us), each slower on the other's count
+    constexpr uint32_t kCap = Q == PULSAR_QUANT_Q6_K ? 3072u : 6144u;
     const uint32_t chunks = (n_pass + RPW - 1u) / RPW;
-    const uint32_t waves = chunks < PK_MV_WAVES ? chunks : PK_MV_WAVES;
+    const uint32_t waves = chunks <= PK_MV_WAVES ? chunks : chunks < kCap ? chunks : kCap;
     const dim3 grid((waves + 3u) / 4u, (n_tok + T - 1u) / T);
     if (lpr_log2 == 6)
         hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 6>), grid, dim3(256), 0, pk::stream(), out, w, xq,
