@@ -451,8 +451,14 @@ static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *
     hipLaunchKernelGGL((mmq_gemm_kernel<Q, RT, C, NT>), dim3((n_tok + 16u * NT - 1u) / (16u * NT),            \
                                                              (out_dim + 16u * RT - 1u) / (16u * RT)),          \
                        dim3(64 * RT * C), 0, pk::stream(), out, w, xq, nb, out_dim, n_tok, row_bytes)
+    // below 8192 rows a 32-row tile leaves CUs idle (4096 rows: 128 blocks);
+    // 16-row tiles with 8 super-blocks per chunk measured fastest there
+    // (Q4_K 4096 x 4096, 16 tokens: 8.7 -> 6.9 us), 32-row tiles with 4
+    // above (Q6_K 8192 x 4096: 11.8 us; 16-row tiles 12.9-14.0 us)
     if (n_tok >= PK_GEMM_NT2)
         PK_GEMM(2, 2, 2);
+    else if (out_dim < 8192u)
+        PK_GEMM(1, 8, 1);
     else
         PK_GEMM(2, 4, 1);
 #undef PK_GEMM
