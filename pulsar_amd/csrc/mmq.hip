@@ -903,8 +903,10 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 for (uint32_t mt = 0; mt < NM; mt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) bsum[mt][r] = 0;
+// two groups unrolled: measured against 1, 4 and 8 (c4 IQ2_XXS layer 197 ->
+// 185 us from 4)
 #ifndef PK_GQ_IQ2_UNROLL
-#define PK_GQ_IQ2_UNROLL 4
+#define PK_GQ_IQ2_UNROLL 2
 #endif
 #pragma unroll PK_GQ_IQ2_UNROLL
                 for (uint32_t g = 0; g < 8; g++) {
