@@ -17,7 +17,7 @@ quantize, gate/up/combine, mid quantize, down [+ grouping, bias]). Inputs are
 resident in HBM before the timed region; weights rotate over >= 2 GB of
 distinct copies / layer banks so the 256 MB Infinity Cache cannot serve them,
 and each layer step routes a different seeded token batch. Timing: HIP events
-on the null stream (the stream every pulsar_* launch uses) bracketing exactly
+on the per-thread default stream (the stream every pulsar_* launch uses) bracketing exactly
 K steps after W warm-up steps, with a device synchronize on both sides.
 
 cpu_baseline: the oracle's C restatement of the reference CPU lane
@@ -59,43 +59,39 @@ def parse_args():
 
 
 class Timer:
-    """HIP events on the launch stream around K steps, two ways: eager
-    launches from Python, and one replay of a HIP graph holding the same K
-    steps (the reference decodes from CUDA graphs too, crates/kernels/src/lib.rs:764-811)."""
+    """HIP events on the launch stream (the per-thread default stream every
+    pulsar_* launch uses) around K steps, two ways: eager launches from
+    Python, and one replay of a HIP graph holding the same K steps, captured
+    on that stream as the reference's decode graphs are
+    (crates/kernels/src/lib.rs:755-811)."""
 
     def __init__(self, torch, K):
-        self.torch, self.K = torch, K
-        assert torch.cuda.current_stream().cuda_stream == 0, "timing assumes the null stream"
+        from pulsar_amd import runtime
+
+        self.torch, self.K, self.rt = torch, K, runtime
 
     def run(self, step, steps: int, warmup: int) -> dict:
-        torch = self.torch
+        rt = self.rt
         for i in range(warmup):
             step(i)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        rt.sync()
+        e0, e1 = rt.Event(), rt.Event()
         e0.record()
         for i in range(steps):
             step(warmup + i)
         e1.record()
-        torch.cuda.synchronize()
-        eager = e0.elapsed_time(e1) / steps
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.K.set_stream(torch.cuda.current_stream())
-            try:
-                for i in range(steps):
-                    step(warmup + i)
-            finally:
-                self.K.set_stream(None)
-        g.replay()  # warm replay
-        torch.cuda.synchronize()
+        e1.synchronize()
+        eager = e0.elapsed_ms(e1) / steps
+        g = rt.Graph.capture(lambda: [step(warmup + i) for i in range(steps)])
+        g.launch()  # warm replay
+        rt.sync()
         e0.record()
-        g.replay()
+        g.launch()
         e1.record()
-        torch.cuda.synchronize()
-        graph = e0.elapsed_time(e1) / steps
+        e1.synchronize()
+        graph = e0.elapsed_ms(e1) / steps
         del g
+        rt.sync()
         return {"ms": graph, "ms_eager": eager}
 
 

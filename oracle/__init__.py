@@ -53,7 +53,10 @@ def load() -> ctypes.CDLL:
         "po_router_select": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _u32, _u32]),
         "po_lcg": (_f32, [ctypes.POINTER(ctypes.c_uint64)]),
         "po_lane_moe": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u64, _u32, _u64, _u32, _u32, _u32]),
-        "po_matmul_kq_mt": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u64, _u32, _u32]),
+        "po_matmul_kq_mt": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u64, _u32, _u32, _vp]),
+        "po_set_simd": (_int, [_int]),
+        "po_rows_dot": (_int, [_vp, _vp, _u64, _u32, _vp, _u32, _u32, _u32, _u32, _vp]),
+        "po_avx2_supported": (_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -135,11 +138,36 @@ def matmul_kq(w: np.ndarray, xq: np.ndarray, in_dim: int, out_dim: int, n_tok: i
     return out if ok else None
 
 
-def matmul_kq_mt(w, xq, in_dim, out_dim, n_tok, row_bytes, quant, threads, out=None):
+def matmul_kq_mt(w, xq, in_dim, out_dim, n_tok, row_bytes, quant, threads, out=None, abs_sum=None):
+    """The threaded dense matvec (256-row jobs); `abs_sum` (f64 [n_tok,
+    out_dim], optional) receives each output's sum_b |f_b|."""
     if out is None:
         out = np.zeros((n_tok, out_dim), dtype=np.float32)
-    ok = load().po_matmul_kq_mt(_p(out), _p(w), _p(xq), in_dim, out_dim, n_tok, row_bytes, quant, threads)
+    ok = load().po_matmul_kq_mt(_p(out), _p(w), _p(xq), in_dim, out_dim, n_tok, row_bytes, quant, threads,
+                                _p(abs_sum))
     return out if ok else None
+
+
+def rows_dot(w, row_bytes, rows, xq, n, n_tok, quant, threads):
+    """(values f32 [n_tok, rows], sum_b |f_b| f64 [n_tok, rows]) of every row
+    of `w` (any format) against n_tok q8_K rows, on `threads` threads."""
+    out = np.zeros((n_tok, rows), dtype=np.float32)
+    abs_sum = np.zeros((n_tok, rows), dtype=np.float64)
+    ok = load().po_rows_dot(_p(out), _p(np.ascontiguousarray(w)), row_bytes, rows, _p(np.ascontiguousarray(xq)),
+                            n, n_tok, quant, threads, _p(abs_sum))
+    if not ok:
+        raise ValueError("po_rows_dot rejected its arguments")
+    return out, abs_sum
+
+
+def set_simd(on: bool) -> bool:
+    """AVX2 row dots for Q4_K / Q2_K / IQ2_XXS on (the default where the CPU
+    has AVX2) or off; returns the previous setting."""
+    return bool(load().po_set_simd(1 if on else 0))
+
+
+def avx2_supported() -> bool:
+    return bool(load().po_avx2_supported())
 
 
 def glu(g: float, u: float, op: int) -> float:

@@ -196,7 +196,7 @@ static float ue4m3(uint8_t e) {
 }
 
 /* cpu:147-156 == cu:1349-1359 (ggml get_scale_min_k4) */
-static void k4_scale_min(uint32_t j, const uint8_t *q, int32_t *sc, int32_t *m) {
+void po_k4_scale_min(uint32_t j, const uint8_t *q, int32_t *sc, int32_t *m) {
     if (j < 4) {
         *sc = q[j] & 63;
         *m = q[j + 4] & 63;
@@ -209,7 +209,7 @@ static void k4_scale_min(uint32_t j, const uint8_t *q, int32_t *sc, int32_t *m) 
 /* IQ2_XXS grid, expanded from the base-3 codes of include/pulsar_iq2xxs_grid.h
  * (digit d_j -> magnitude {8, 25, 43}[d_j] in byte j). */
 static const uint16_t k_iq2xxs_codes[256] = {PULSAR_IQ2XXS_GRID_CODES};
-static uint8_t iq2xxs_mag(uint32_t idx, uint32_t j) {
+uint32_t po_iq2xxs_mag(uint32_t idx, uint32_t j) {
     static const uint8_t mags[3] = {8, 25, 43};
     uint32_t c = k_iq2xxs_codes[idx];
     for (uint32_t k = 0; k < j; k++) c /= 3u;
@@ -251,8 +251,8 @@ float po_block_dot(uint32_t quant, const uint8_t *row, uint32_t b,
         int32_t isum = 0, msum = 0;
         for (uint32_t j = 0; j < 4; j++) {
             int32_t sc1, m1, sc2, m2;
-            k4_scale_min(2 * j, scales, &sc1, &m1);
-            k4_scale_min(2 * j + 1, scales, &sc2, &m2);
+            po_k4_scale_min(2 * j, scales, &sc1, &m1);
+            po_k4_scale_min(2 * j + 1, scales, &sc2, &m2);
             int32_t s1 = 0, s2 = 0;
             for (uint32_t i = 0; i < 32; i++) {
                 const uint8_t v = q4[32 * j + i];
@@ -342,7 +342,7 @@ float po_block_dot(uint32_t quant, const uint8_t *row, uint32_t b,
                 const uint32_t gi = (aux0 >> (8 * k)) & 0xffu;
                 const uint32_t sm = sign_mask((aux1 >> (7 * k)) & 127u);
                 for (uint32_t i = 0; i < 8; i++) {
-                    const int32_t g = iq2xxs_mag(gi, i);
+                    const int32_t g = po_iq2xxs_mag(gi, i);
                     const int32_t w = ((sm >> i) & 1u) ? -g : g;
                     sumi += w * q8[32 * ib32 + 8 * k + i];
                 }
@@ -385,8 +385,8 @@ float po_block_dot(uint32_t quant, const uint8_t *row, uint32_t b,
         int32_t isum = 0, msum = 0;
         for (uint32_t j = 0; j < 4; j++) {
             int32_t sc1, m1, sc2, m2;
-            k4_scale_min(2 * j, blk + 4, &sc1, &m1);
-            k4_scale_min(2 * j + 1, blk + 4, &sc2, &m2);
+            po_k4_scale_min(2 * j, blk + 4, &sc1, &m1);
+            po_k4_scale_min(2 * j + 1, blk + 4, &sc2, &m2);
             int32_t s1 = 0, s2 = 0;
             for (uint32_t i = 0; i < 32; i++) {
                 const int32_t h1 = (qh[i] >> (2 * j)) & 1, h2 = (qh[i] >> (2 * j + 1)) & 1;
@@ -677,9 +677,26 @@ static uint32_t valid32_in_sb(uint32_t n, uint32_t b) {
     return rem >= 256u ? 8u : (rem + 31u) / 32u;
 }
 
+/* AVX2 row dots of the lane formats (lane_avx2.c): on by default where the
+ * CPU has AVX2, like the reference lane's dispatch (cpu:76-86, 242-247,
+ * 721-726); bit-identical to the scalar dots. */
+int po_avx2_supported(void);
+int po_avx2_has_format(uint32_t quant);
+float po_avx2_vec_dot(uint32_t quant, const uint8_t *row, const pulsar_block_q8_K *xq, uint32_t n);
+static int g_simd = -1;
+
+int po_set_simd(int on) {
+    const int prev = g_simd < 0 ? po_avx2_supported() : g_simd;
+    g_simd = on && po_avx2_supported();
+    return prev;
+}
+
 /* cpu:242-279 (and siblings): total = 0; total += f_b for b in order */
 float po_vec_dot(uint32_t quant, const uint8_t *row, const pulsar_block_q8_K *xq,
                  uint32_t n, double *abs_sum) {
+    if (g_simd < 0) g_simd = po_avx2_supported();
+    if (g_simd && !abs_sum && n % 256u == 0 && po_avx2_has_format(quant))
+        return po_avx2_vec_dot(quant, row, xq, n);
     const uint32_t nb = (n + 255u) / 256u;
     float total = 0.0f;
     double as = 0.0;
@@ -706,7 +723,7 @@ void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out)
             const double xmin = po_f16_to_f32(rd16(blk + 2));
             for (uint32_t s = 0; s < 8; s++) { /* sub-block s: values 32s.. */
                 int32_t sc, m;
-                k4_scale_min(s, blk + 4, &sc, &m);
+                po_k4_scale_min(s, blk + 4, &sc, &m);
                 for (uint32_t i = 0; i < 32; i++) {
                     const uint8_t byte = blk[16 + 32 * (s / 2) + i];
                     const int32_t q = (s & 1) ? (byte >> 4) : (byte & 0x0f);
@@ -756,7 +773,7 @@ void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out)
                 for (uint32_t k = 0; k < 4; k++) {
                     const uint32_t sm = sign_mask((aux1 >> (7 * k)) & 127u);
                     for (uint32_t i = 0; i < 8; i++) {
-                        const double mag = iq2xxs_mag((aux0 >> (8 * k)) & 0xffu, i);
+                        const double mag = po_iq2xxs_mag((aux0 >> (8 * k)) & 0xffu, i);
                         v[32 * g + 8 * k + i] = ((sm >> i) & 1u) ? -db * mag : db * mag;
                     }
                 }
@@ -785,7 +802,7 @@ void po_dequant_row(uint32_t quant, const uint8_t *row, uint32_t n, double *out)
             const double xd = po_f16_to_f32(rd16(blk)), xmin = po_f16_to_f32(rd16(blk + 2));
             for (uint32_t s = 0; s < 8; s++) {
                 int32_t sc, m;
-                k4_scale_min(s, blk + 4, &sc, &m);
+                po_k4_scale_min(s, blk + 4, &sc, &m);
                 for (uint32_t i = 0; i < 32; i++) {
                     const uint8_t byte = blk[48 + 32 * (s / 2) + i];
                     const int32_t lo = (s & 1) ? (byte >> 4) : (byte & 0x0f);
@@ -1248,6 +1265,7 @@ static void pool_run(uint32_t threads, po_job_fn fn, void *ctx, uint32_t n_jobs)
 
 typedef struct {
     float *out;
+    double *abs_sum;
     const uint8_t *w;
     const pulsar_block_q8_K *xq;
     uint32_t in_dim, out_dim, n_tok, quant;
@@ -1260,19 +1278,32 @@ static void mv_job(void *vctx, uint32_t job) {
     const uint32_t lo = job * 256u;
     const uint32_t hi = lo + 256u < c->out_dim ? lo + 256u : c->out_dim;
     for (uint32_t r = lo; r < hi; r++)
-        for (uint32_t t = 0; t < c->n_tok; t++)
-            c->out[(uint64_t)t * c->out_dim + r] = po_vec_dot(
-                    c->quant, c->w + (uint64_t)r * c->row_bytes, c->xq + (uint64_t)t * nb, c->in_dim, NULL);
+        for (uint32_t t = 0; t < c->n_tok; t++) {
+            const uint64_t o = (uint64_t)t * c->out_dim + r;
+            c->out[o] = po_vec_dot(c->quant, c->w + (uint64_t)r * c->row_bytes, c->xq + (uint64_t)t * nb,
+                                   c->in_dim, c->abs_sum ? c->abs_sum + o : NULL);
+        }
+}
+
+int po_rows_dot(float *out, const uint8_t *w, uint64_t row_bytes, uint32_t rows,
+                const pulsar_block_q8_K *xq, uint32_t n, uint32_t n_tok, uint32_t quant,
+                uint32_t threads, double *abs_sum) {
+    if (n == 0 || rows == 0 || n_tok == 0 || row_bytes == 0 || !quant_ok(quant) ||
+        (quant != PULSAR_QUANT_MXFP4 && n % 256u != 0) || (quant == PULSAR_QUANT_MXFP4 && n % 32u != 0))
+        return 0;
+    mv_ctx c = {out, abs_sum, w, xq, n, rows, n_tok, quant, row_bytes};
+    pool_run(threads, mv_job, &c, (rows + 255u) / 256u);
+    return 1;
 }
 
 int po_matmul_kq_mt(float *out, const uint8_t *w, const pulsar_block_q8_K *xq,
                     uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
-                    uint64_t row_bytes, uint32_t quant, uint32_t threads) {
+                    uint64_t row_bytes, uint32_t quant, uint32_t threads, double *abs_sum) {
     quant &= ~PULSAR_QUANT_A4_OK;
     if (in_dim == 0 || in_dim % 256u != 0 || out_dim == 0 || n_tok == 0 || row_bytes == 0 ||
         !quant_ok(quant) || quant == PULSAR_QUANT_MXFP4)
         return 0;
-    mv_ctx c = {out, w, xq, in_dim, out_dim, n_tok, quant, row_bytes};
+    mv_ctx c = {out, abs_sum, w, xq, in_dim, out_dim, n_tok, quant, row_bytes};
     pool_run(threads, mv_job, &c, (out_dim + 255u) / 256u);
     return 1;
 }

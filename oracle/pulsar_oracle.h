@@ -101,10 +101,25 @@ int po_lane_moe(float *out, const pulsar_expert_ptrs *ptrs, const float *weights
                 uint32_t gate_quant, uint64_t down_row_bytes, uint32_t down_quant,
                 uint32_t act_op, uint32_t threads);
 
-/* Multi-threaded dense matvec (rows split in 256-row jobs) for the baseline. */
+/* Multi-threaded dense matvec (rows split in 256-row jobs, like the Lane's
+ * gate/up jobs) for the baseline and for large parity checks; abs_sum
+ * (nullable, f64 [n_tok][out_dim]) receives each output's sum_b |f_b|. */
 int po_matmul_kq_mt(float *out, const uint8_t *w, const pulsar_block_q8_K *xq,
                     uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
-                    uint64_t row_bytes, uint32_t quant, uint32_t threads);
+                    uint64_t row_bytes, uint32_t quant, uint32_t threads, double *abs_sum);
+
+/* The same for any format (MXFP4 rows included, n a multiple of 32 there,
+ * of 256 otherwise): out[t][r] = po_vec_dot(row r, xq[t]) over `rows` rows
+ * row_bytes apart. The checker of full-shape expert stages. */
+int po_rows_dot(float *out, const uint8_t *w, uint64_t row_bytes, uint32_t rows,
+                const pulsar_block_q8_K *xq, uint32_t n, uint32_t n_tok, uint32_t quant,
+                uint32_t threads, double *abs_sum);
+
+/* Selects the AVX2 row dots of the lane formats (Q4_K, Q2_K, IQ2_XXS) in
+ * po_vec_dot when on != 0 and the CPU has AVX2 (the default), the scalar
+ * dots otherwise; returns the previous setting. Both give the same bits. A
+ * request for abs_sum always takes the scalar dots. */
+int po_set_simd(int on);
 
 #ifdef __cplusplus
 }

@@ -17,8 +17,9 @@ namespace pk {
 
 constexpr uint32_t kWave = 64;
 
-// Stream of every launch made by the calling thread (pulsar_set_stream;
-// the null stream by default, like the reference's launches).
+// Stream of every launch made by the calling thread: its per-thread
+// default stream (hipStreamPerThread), as the reference's launches use
+// cudaStreamPerThread, unless pulsar_set_stream selected another.
 hipStream_t stream();
 
 // Error reporting with the reference's message shape (pulsar_kernels.cu:25-29).

@@ -115,6 +115,14 @@ PK_DEV void stage_q8_rows(uint8_t *lds, uint32_t m, uint32_t k_blocks, RowFn src
     }
 }
 
+// Row value pieces (defined below): row_partial leaves each super-block's
+// value in its quad's last lane, row_finish sums them into the row group's
+// last lane.
+template <uint32_t Q, uint32_t UPLMAX>
+PK_DEV float row_partial(bool row_ok, const RowGeom &rg, const typename Fmt<Q>::W (&w)[UPLMAX],
+                         const Act (&a)[UPLMAX], const uint2 *lut);
+PK_DEV float row_finish(float acc, const RowGeom &rg);
+
 // Loads this lane's weight units of one row. Loads are unconditional: a
 // lane whose unit does not exist reads the row's last unit instead (in
 // bounds) and row_partial masks its contribution; callers likewise pass a

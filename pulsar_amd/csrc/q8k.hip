@@ -3,7 +3,12 @@
 
 namespace pk {
 
-static thread_local hipStream_t g_stream = nullptr;
+// The calling thread's per-thread default stream unless pulsar_set_stream
+// chose another: the reference builds with --default-stream=per-thread
+// (crates/kernels/build.rs:42-48), so its launches land on
+// cudaStreamPerThread, where Graph::capture records them
+// (crates/kernels/src/lib.rs:755-790).
+static thread_local hipStream_t g_stream = hipStreamPerThread;
 hipStream_t stream() { return g_stream; }
 
 // One wave per 256-value block (quantize_block_wave).
@@ -54,6 +59,6 @@ extern "C" int pulsar_bw_read(void *buf, uint64_t bytes, void *sink) {
 }
 
 extern "C" int pulsar_set_stream(void *stream) {
-    pk::g_stream = (hipStream_t)stream;
+    pk::g_stream = stream ? (hipStream_t)stream : hipStreamPerThread;
     return 1;
 }

@@ -4,8 +4,10 @@ Each function has the reference wrapper's name and argument order, takes
 device buffers (torch CUDA tensors or raw device addresses as ints) and raises
 KernelError(op) where the Rust wrapper returns Err(Error(op)) (the C entry
 point returned 0; crates/kernels/src/lib.rs:212-218). Launches are
-asynchronous on the null stream; call torch.cuda.synchronize() (the
-reference's kernels::sync) before reading results on the host.
+asynchronous on the calling thread's per-thread default stream (the
+reference's --default-stream=per-thread); call runtime.sync() or
+torch.cuda.synchronize() (the reference's kernels::sync) before reading
+results on the host.
 """
 from __future__ import annotations
 
@@ -232,8 +234,9 @@ def router_selftest() -> bool:
 
 
 def set_stream(stream) -> None:
-    """Routes later launches from this thread to `stream` (a torch Stream, a
-    raw hipStream_t int, or None for the null stream)."""
+    """Routes later launches from this thread to `stream` (a torch Stream or
+    a raw hipStream_t int); None (or torch's null stream) restores the
+    per-thread default stream."""
     handle = 0 if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
     _check(_lib.load().pulsar_set_stream(handle or None), "set_stream")
 

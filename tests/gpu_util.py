@@ -7,6 +7,9 @@ HIP kernels sum the per-super-block fp32 values in a different order than
 the CPU lane, so |gpu - oracle| <= TOL_REL * sum_b |f_b| (+ TOL_ABS), with
 sum_b |f_b| the oracle's condition-aware scale and TOL_REL = 1e-5.
 """
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -57,3 +60,25 @@ def assert_rows_close(got, want, scale, what=""):
         f"max err {err.max():.3e}, max rel {(err / np.maximum(scale, 1e-30)).max():.3e}"
     )
     return float(err.max()), float((err / np.maximum(scale, 1e-30)).max())
+
+
+def parity_stats(got, want, scale) -> dict:
+    """Achieved error of fp32 outputs against the oracle: max |gpu - oracle|,
+    max |delta| / sum_b |f_b| (the bound the tests assert) and the
+    reference's own |delta| / max(|ref|, 1) (crates/kernels/src/lib.rs:2054)."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    w = np.asarray(want, np.float64).reshape(-1)
+    sc = np.asarray(scale, np.float64).reshape(-1)
+    err = np.abs(g - w)
+    return {"n": int(err.size), "max_abs": float(err.max()),
+            "max_rel_sum_abs": float((err / np.maximum(sc, 1e-30)).max()),
+            "max_rel_ref": float((err / np.maximum(np.abs(w), 1.0)).max())}
+
+
+def record_parity(config: str, stats: dict) -> None:
+    """Appends one JSON line {config, stats} to $PULSAR_PARITY_LOG when set
+    (the achieved-error table of the parity runs)."""
+    path = os.environ.get("PULSAR_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"config": config, **stats}) + "\n")

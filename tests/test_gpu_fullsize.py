@@ -1,0 +1,357 @@
+"""Parity at the benchmark configurations' full shapes, against the oracle.
+
+Dense matvec (pulsar_matmul_kq): config 1 (Q4_K 4096x4096) and config 2
+(Q6_K 8192x4096) at decode batch 1 and as a 16-token chunk, matrices whose
+row passes exceed the decode kernel's wave grid (Q6_K 32768 rows over 3072
+waves, Q4_K / Q2_K / IQ2_XXS 16384 rows over 6144), the MFMA chunk kernel's
+32-row tiles at 8 tokens, a 64-token prefill tile, and a Q6_K lm-head of
+151,936 rows (the reference runs its head through matmul_kq,
+crates/engine/src/lib.rs:7092-7099). Two forms each: unit weight and
+activation scales, where every output is an exact integer (compared with
+==), and seeded weights of the stated distributions, compared within
+|delta| <= 1e-5 * sum_b |f_b|. This is the reference's own check of its
+GEMM against a reference path (crates/kernels/src/lib.rs:1998-2065).
+
+Routed-MoE layers (configs 3, 4 and 5) at full shape through the entry
+points the benchmark times: router logits against the oracle's f32 GEMV,
+the routing of those logits equal to the oracle's, the gate/up stage
+against the oracle within its bound, and the down stage on the oracle's own
+mid q8_K (the stated way to separate a mid rounding flip from a kernel
+error), with the slot sum in slot order.
+
+Each fp32 comparison records its achieved error when $PULSAR_PARITY_LOG
+names a file (tests/gpu_util.record_parity).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from pulsar_amd import formats as fm
+from pulsar_amd import kernels as K
+from pulsar_amd import synth
+from pulsar_amd.formats import QUANT_IQ2_XXS, QUANT_Q2_K, QUANT_Q4_K, QUANT_Q6_K, q8k_blocks, row_bytes
+from tests.gpu_util import TOL_REL, down, parity_stats, record_parity, up, up_f32, zeros_f32
+
+pytestmark = pytest.mark.gpu
+THREADS = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else 8))
+
+DENSE_FULL = [
+    # name, quant, rows, cols, n_tok
+    ("c1_q4k_4096x4096_t1", QUANT_Q4_K, 4096, 4096, 1),
+    ("c1_q4k_4096x4096_t16", QUANT_Q4_K, 4096, 4096, 16),
+    ("c2_q6k_8192x4096_t1", QUANT_Q6_K, 8192, 4096, 1),
+    ("c2_q6k_8192x4096_t16", QUANT_Q6_K, 8192, 4096, 16),
+    ("q6k_32768x4096_t1_grid_loop", QUANT_Q6_K, 32768, 4096, 1),
+    ("q4k_16384x4096_t1_grid_loop", QUANT_Q4_K, 16384, 4096, 1),
+    ("q2k_16384x4096_t1_grid_loop", QUANT_Q2_K, 16384, 4096, 1),
+    ("iq2xxs_16384x4096_t1_grid_loop", QUANT_IQ2_XXS, 16384, 4096, 1),
+    ("q6k_16384x4096_t8_mfma32", QUANT_Q6_K, 16384, 4096, 8),
+    ("q6k_8192x4096_t2", QUANT_Q6_K, 8192, 4096, 2),
+    ("q4k_8192x4096_t4", QUANT_Q4_K, 8192, 4096, 4),
+    ("q4k_4096x4096_t64_prefill", QUANT_Q4_K, 4096, 4096, 64),
+]
+
+
+def _unit_scales(quant, w):
+    """Sets every f16 weight scale (and min) of the blocks to 1.0 (IQ2_XXS:
+    8.0, so 0.125 * d = 1)."""
+    bb = fm.BLOCK_LAYOUT[quant][1]
+    blk = w.reshape(w.shape[0], -1, bb)
+    d_off, m_off, d_val = {QUANT_Q4_K: (0, 2, 0x3C00), QUANT_Q2_K: (80, 82, 0x3C00),
+                           QUANT_Q6_K: (208, None, 0x3C00), QUANT_IQ2_XXS: (0, None, 0x4800)}[quant]
+    blk[..., d_off], blk[..., d_off + 1] = d_val & 0xFF, d_val >> 8
+    if m_off is not None:
+        blk[..., m_off], blk[..., m_off + 1] = 0x00, 0x3C
+    return w
+
+
+def _unit_xq(n_tok, n, rng):
+    """q8_K rows with d = 1 and quants in [-40, 40] (consistent bsums)."""
+    nb = n // 256
+    qs = rng.integers(-40, 41, (n_tok, nb, 256)).astype(np.int8)
+    blk = np.zeros((n_tok, nb, 292), np.uint8)
+    blk[..., 0:4] = np.array([1.0], np.float32).view(np.uint8)
+    blk[..., 4:260] = qs.view(np.uint8)
+    bs = qs.reshape(n_tok, nb, 16, 16).astype(np.int16).sum(-1).astype(np.int16)
+    blk[..., 260:292] = bs.view(np.uint8).reshape(n_tok, nb, 32)
+    return blk.reshape(n_tok, nb * 292)
+
+
+@pytest.mark.parametrize("name,quant,rows,cols,n_tok", DENSE_FULL, ids=[c[0] for c in DENSE_FULL])
+def test_dense_full_shape(dev, name, quant, rows, cols, n_tok):
+    rng = np.random.default_rng(rows + n_tok)
+    rb = row_bytes(quant, cols)
+    w = synth.quant_matrix(quant, rows, cols, synth.rng_for(rows * 7 + n_tok, name))
+    w_d = up(w)
+    out = zeros_f32((n_tok, rows))
+    # seeded weights, N(0,1) activations: within 1e-5 * sum_b |f_b|
+    xq = oracle.quantize_q8_k(synth.activations(n_tok, cols, synth.rng_for(3, name)))
+    K.matmul_kq(out, w_d, up(xq), cols, rows, n_tok, rb, quant)
+    got = down(out)
+    want, scale = oracle.rows_dot(w, rb, rows, xq, cols, n_tok, quant, THREADS)
+    st = parity_stats(got, want, scale)
+    record_parity(name, st)
+    assert st["max_rel_sum_abs"] <= TOL_REL, st
+    # unit scales: every output an exact integer, bit-exact
+    _unit_scales(quant, w)
+    xq1 = _unit_xq(n_tok, cols, rng)
+    w_d.copy_(torch.from_numpy(w.reshape(-1)))
+    out.zero_()
+    K.matmul_kq(out, w_d, up(xq1), cols, rows, n_tok, rb, quant)
+    got1 = down(out)
+    want1, _ = oracle.rows_dot(w, rb, rows, xq1, cols, n_tok, quant, THREADS)
+    assert np.abs(want1).max() < 2**24  # every partial sum exact in fp32
+    assert np.array_equal(got1, want1), f"{name}: {np.count_nonzero(got1 != want1)} integer outputs differ"
+
+
+def test_lm_head_q6k_decode(dev):
+    """A vocab-sized Q6_K head (151,936 x 4096, the Qwen vocabulary) at batch 1."""
+    name, quant, rows, cols = "lm_head_q6k_151936x4096_t1", QUANT_Q6_K, 151936, 4096
+    rb = row_bytes(quant, cols)
+    w = synth.quant_matrix(quant, rows, cols, synth.rng_for(5, name))
+    xq = oracle.quantize_q8_k(synth.activations(1, cols, synth.rng_for(6, name)))
+    out = zeros_f32((1, rows))
+    K.matmul_kq(out, up(w), up(xq), cols, rows, 1, rb, quant)
+    got = down(out)
+    want, scale = oracle.rows_dot(w, rb, rows, xq, cols, 1, quant, THREADS)
+    st = parity_stats(got, want, scale)
+    record_parity(name, st)
+    assert st["max_rel_sum_abs"] <= TOL_REL, st
+
+
+# --------------------------------------------------------------- MoE layers --
+
+class FullLayer:
+    """One layer of a benchmark MoE configuration on host and device."""
+
+    def __init__(self, spec: synth.MoESpec, seed=21):
+        self.s = s = spec
+        self.bank = b = synth.moe_bank(spec, seed=seed)
+        self.dev = {k: up(np.concatenate([getattr(b, k).reshape(-1), np.zeros(256, np.uint8)]))
+                    for k in ("gate", "up", "down")}
+        for k in ("router_b", "gate_b", "up_b", "down_b"):
+            a = getattr(b, k)
+            self.dev[k] = None if a is None else up_f32(a)
+        self.dev["router_w"] = up_f32(b.router_w)
+        self.shared_dev = None
+        if s.shared:
+            self.shared_dev = [up(np.concatenate([a.reshape(-1), np.zeros(256, np.uint8)]))
+                               for a in (b.sh_gate, b.sh_up, b.sh_down)]
+        self.gsz, self.dsz = s.ffn * s.gate_row_bytes, s.hidden * s.down_row_bytes
+
+    def desc(self):
+        d = self.dev
+        s = self.s
+        p = [None if d[k] is None else d[k].data_ptr() for k in ("gate_b", "up_b", "down_b")]
+        return K.ExpertBank(d["gate"].data_ptr(), d["up"].data_ptr(), d["down"].data_ptr(), *p,
+                            self.gsz, self.gsz, self.dsz, s.ffn, s.ffn, s.hidden)
+
+    def shared(self):
+        return [tuple(t.data_ptr() for t in self.shared_dev)] if self.shared_dev else None
+
+    def host_slot(self, e):
+        """(gate, up, down, gate_b, up_b, down_b) host arrays of routed
+        expert e, or of the shared expert for e == -2."""
+        b = self.bank
+        if e == -2:
+            return (b.sh_gate, b.sh_up, b.sh_down, None, None, None)
+        bias = [None if a is None else a[e] for a in (b.gate_b, b.up_b, b.down_b)]
+        return (b.gate[e], b.up[e], b.down[e], *bias)
+
+
+def _route_and_check(L: FullLayer, x_d, n_tok):
+    """router_logits_q8 against the oracle, then the oracle's routing of the
+    GPU logits: returns (logits, xq (device), host slots [n_tok][n_slots]
+    as expert ids with -2 = shared, slot weights f32 [n_tok][n_slots])."""
+    s = L.s
+    logits = zeros_f32((n_tok, s.n_expert))
+    xq_d = torch.zeros(n_tok * q8k_blocks(s.hidden) * 292, dtype=torch.uint8, device="cuda")
+    K.router_logits_q8(logits, xq_d, x_d, L.dev["router_w"], L.dev["router_b"], s.hidden, s.n_expert, n_tok)
+    lg = down(logits)
+    x = down(x_d)
+    want = oracle.matmul_f32(L.bank.router_w, x, s.hidden, s.n_expert, n_tok)
+    if L.bank.router_b is not None:
+        want = oracle.add_bias_rows(want, L.bank.router_b, s.n_expert, n_tok)
+    # fp32 GEMV, sum order differs: within 1e-5 of sum |w x| (+ |bias|)
+    ab = np.abs(L.bank.router_w).astype(np.float64) @ np.abs(x.astype(np.float64)).T
+    if L.bank.router_b is not None:
+        ab = ab + np.abs(L.bank.router_b.astype(np.float64))[:, None]
+    st = parity_stats(lg, want, ab.T)
+    record_parity(s.name + "/router_logits", st)
+    assert st["max_rel_sum_abs"] <= TOL_REL, st
+    assert np.array_equal(down(xq_d).reshape(n_tok, -1), oracle.quantize_q8_k(x))  # q8_K bit-exact
+    sel, rw = oracle.router_select(lg, None, s.n_expert, s.k_used, 1.0, n_tok, 1, 0)
+    slots = np.concatenate([sel, np.full((n_tok, 1), -2)], axis=1) if s.shared else sel
+    sw = np.concatenate([rw, np.ones((n_tok, 1), np.float32)], axis=1) if s.shared else rw
+    return logits, xq_d, slots, np.ascontiguousarray(sw, np.float32)
+
+
+def _oracle_pair(L: FullLayer, slots, sw, xq):
+    """Oracle mid rows and their tolerance bound, one (token, slot) at a time
+    through the threaded row dots."""
+    s = L.s
+    n_tok, n_slots = slots.shape
+    mid = np.zeros((n_tok * n_slots, s.ffn), np.float32)
+    bound = np.zeros_like(mid, dtype=np.float64)
+    for t in range(n_tok):
+        for j in range(n_slots):
+            g_w, u_w, _, gb, ub, _ = L.host_slot(int(slots[t, j]))
+            g, ag = oracle.rows_dot(g_w, s.gate_row_bytes, s.ffn, xq[t:t + 1], s.hidden, 1, s.gate_quant, THREADS)
+            u, au = oracle.rows_dot(u_w, s.gate_row_bytes, s.ffn, xq[t:t + 1], s.hidden, 1, s.gate_quant, THREADS)
+            g, u, ag, au = g[0], u[0], ag[0], au[0]
+            if gb is not None:
+                g = (g + gb).astype(np.float32)
+                u = (u + ub).astype(np.float32)
+            w = sw[t, j]
+            mid[t * n_slots + j] = [oracle.glu(float(a), float(c), s.act_op) * w for a, c in zip(g, u)]
+            bound[t * n_slots + j] = TOL_REL * w * (1.5 * (np.abs(u) + 1) * ag + (np.abs(g) + 1) * au)
+    return mid, bound + 4e-7 * np.abs(mid) + 1e-30
+
+
+def _oracle_down(L: FullLayer, slots, midq):
+    s = L.s
+    n_tok, n_slots = slots.shape
+    mb = q8k_blocks(s.ffn) * 292
+    out = np.zeros((n_tok, s.hidden), np.float32)
+    scale = np.zeros((n_tok, s.hidden), np.float64)
+    parts = np.zeros((n_tok, n_slots, s.hidden), np.float32)
+    for t in range(n_tok):
+        for j in range(n_slots):
+            d_w = L.host_slot(int(slots[t, j]))[2]
+            q = midq[t * n_slots + j].reshape(1, mb)
+            v, a = oracle.rows_dot(d_w, s.down_row_bytes, s.hidden, q, s.ffn, 1, s.down_quant, THREADS)
+            parts[t, j] = v[0]
+            scale[t] += a[0]
+    for j in range(n_slots):
+        out += parts[:, j]
+    return out, scale
+
+
+def _check(name, got, want, bound_or_scale, is_bound):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    if is_bound:
+        assert (err <= bound_or_scale).all(), f"{name}: max err {err.max():.3e}, worst ratio " \
+                                              f"{(err / bound_or_scale).max():.2f}"
+        record_parity(name, {"n": int(err.size), "max_abs": float(err.max()),
+                             "max_ratio_to_bound": float((err / bound_or_scale).max()),
+                             "max_rel_ref": float((err / np.maximum(np.abs(want), 1.0)).max())})
+    else:
+        st = parity_stats(got, want, bound_or_scale)
+        record_parity(name, st)
+        assert st["max_rel_sum_abs"] <= TOL_REL, (name, st)
+
+
+def test_c3_decode_layer_full_shape(dev):
+    """Config 3 through the fused decode layer the benchmark times:
+    router_logits_q8 -> moe_pair_routed -> moe_down_f32 (top-8 of 256 plus
+    the shared expert, Q4_K gate/up, Q6_K down)."""
+    s = synth.C3
+    L = FullLayer(s)
+    x_d = up_f32(synth.activations(1, s.hidden, synth.rng_for(9, s.name)))
+    logits, xq_d, slots, sw = _route_and_check(L, x_d, 1)
+    n_slots = s.n_slots
+    mid = zeros_f32((n_slots, s.ffn))
+    ptrs = torch.zeros(n_slots * 48, dtype=torch.uint8, device="cuda")
+    slot_w = zeros_f32((1, n_slots))
+    sel = torch.zeros((1, s.k_used), dtype=torch.int32, device="cuda")
+    rw = zeros_f32((1, s.k_used))
+    K.moe_pair_routed(mid, ptrs, slot_w, sel, rw, logits, None, s.n_expert, s.k_used, 1.0, 1, L.desc(), L.shared(),
+                      xq_d, s.hidden, s.ffn, 1, s.gate_row_bytes, s.gate_quant, s.act_op)
+    assert np.array_equal(down(sel), slots[:, :s.k_used])
+    np.testing.assert_allclose(down(slot_w), sw, rtol=1e-6)
+    xq = down(xq_d).reshape(1, -1)
+    want_mid, bound = _oracle_pair(L, slots, down(slot_w), xq)
+    _check(s.name + "/pair", down(mid), want_mid, bound, True)
+    # down on the oracle's own mids (moe_down_f32 quantizes them itself)
+    out = zeros_f32((1, s.hidden))
+    K.moe_down_f32(out, ptrs, slot_w, up_f32(want_mid), s.ffn, s.hidden, n_slots, 1, s.down_row_bytes,
+                   s.down_quant, False)
+    want, scale = _oracle_down(L, slots, oracle.quantize_q8_k(want_mid))
+    _check(s.name + "/down", down(out), want, scale, False)
+
+
+@pytest.mark.parametrize("spec", [synth.C4_Q2K, synth.C4_IQ2, synth.C5_B64], ids=lambda s: s.name)
+def test_grouped_chunk_layer_full_shape(dev, spec):
+    """Configs 4 (16 tokens, top-8 of 128, Q2_K / IQ2_XXS) and 5 at 64
+    tokens (MXFP4, biases, swiglu_oai) through the grouped path the benchmark
+    times: router_logits_q8 -> moe_route_group -> grouped pair -> quantize ->
+    grouped down -> slot sum (+ down bias)."""
+    s = spec
+    L = FullLayer(s)
+    n_tok, n_slots = s.n_tok, s.n_slots
+    x_d = up_f32(synth.activations(n_tok, s.hidden, synth.rng_for(9, s.name)))
+    logits, xq_d, slots, sw = _route_and_check(L, x_d, n_tok)
+    max_groups = min(s.n_expert, n_tok * n_slots)
+    f32 = dict(dtype=torch.float32, device="cuda")
+    sel = torch.zeros((n_tok, s.k_used), dtype=torch.int32, device="cuda")
+    rw = zeros_f32((n_tok, s.k_used))
+    ptrs = torch.zeros(n_tok * n_slots * 48, dtype=torch.uint8, device="cuda")
+    slot_w = zeros_f32((n_tok, n_slots))
+    gptrs = torch.zeros(max_groups * 48, dtype=torch.uint8, device="cuda")
+    starts = torch.zeros(max_groups + 1, dtype=torch.int32, device="cuda")
+    pairs = torch.zeros(n_tok * n_slots, dtype=torch.int32, device="cuda")
+    K.moe_route_group(sel, rw, ptrs, slot_w, gptrs, starts, pairs, logits, None, s.n_expert, s.k_used, 1.0, 1,
+                      L.desc(), L.shared(), n_tok, max_groups)
+    assert np.array_equal(down(sel), slots)
+    np.testing.assert_allclose(down(slot_w), sw, rtol=1e-6)
+    mid = torch.zeros((n_tok * n_slots, s.ffn), **f32)
+    K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq_d, s.hidden, s.ffn, n_slots, max_groups,
+                              s.gate_row_bytes, s.gate_quant, s.act_op)
+    xq = down(xq_d).reshape(n_tok, -1)
+    want_mid, bound = _oracle_pair(L, slots, down(slot_w), xq)
+    _check(s.name + "/pair", down(mid), want_mid, bound, True)
+    midq = oracle.quantize_q8_k(want_mid)
+    partial = torch.zeros((n_tok * n_slots, s.hidden), **f32)
+    K.moe_down_grouped(partial, gptrs, starts, pairs, up(midq), s.ffn, s.hidden, n_slots, max_groups,
+                       s.down_row_bytes, s.down_quant)
+    out = torch.zeros((n_tok, s.hidden), **f32)
+    K.moe_slot_sum(out, partial, s.hidden, n_slots, n_tok)
+    want, scale = _oracle_down(L, slots, midq)
+    _check(s.name + "/down", down(out), want, scale, False)
+    p = down(partial).reshape(n_tok, n_slots, s.hidden)
+    acc = np.zeros((n_tok, s.hidden), np.float32)
+    for j in range(n_slots):
+        acc += p[:, j]
+    assert np.array_equal(down(out), acc)  # slot sum in slot order
+    if s.biases:
+        # down bias, bit-exact against the oracle's formula
+        hptrs = oracle.host_ptrs([L.host_slot(int(e)) for e in slots.reshape(-1)])
+        biased = out.clone()
+        K.moe_down_bias(biased, ptrs, slot_w, s.hidden, n_slots, n_tok)
+        want_b = oracle.moe_down_bias(down(out), hptrs, down(slot_w), s.hidden, n_slots, n_tok)
+        assert np.array_equal(down(biased), want_b)
+
+
+def test_c5_decode_layer_full_shape(dev):
+    """Config 5 at batch 1 through the path the benchmark times:
+    router_logits_q8 -> moe_pair_routed -> quantize_q8_K -> moe_down_biased."""
+    s = synth.C5_B1
+    L = FullLayer(s)
+    x_d = up_f32(synth.activations(1, s.hidden, synth.rng_for(9, s.name)))
+    logits, xq_d, slots, sw = _route_and_check(L, x_d, 1)
+    n_slots = s.n_slots
+    mid = zeros_f32((n_slots, s.ffn))
+    ptrs = torch.zeros(n_slots * 48, dtype=torch.uint8, device="cuda")
+    slot_w = zeros_f32((1, n_slots))
+    sel = torch.zeros((1, s.k_used), dtype=torch.int32, device="cuda")
+    rw = zeros_f32((1, s.k_used))
+    K.moe_pair_routed(mid, ptrs, slot_w, sel, rw, logits, None, s.n_expert, s.k_used, 1.0, 1, L.desc(), None,
+                      xq_d, s.hidden, s.ffn, 1, s.gate_row_bytes, s.gate_quant, s.act_op)
+    assert np.array_equal(down(sel), slots)
+    xq = down(xq_d).reshape(1, -1)
+    want_mid, bound = _oracle_pair(L, slots, down(slot_w), xq)
+    _check(s.name + "/pair", down(mid), want_mid, bound, True)
+    midq = oracle.quantize_q8_k(want_mid)
+    out = zeros_f32((1, s.hidden))
+    K.moe_down_biased(out, ptrs, slot_w, up(midq), s.ffn, s.hidden, n_slots, 1, s.down_row_bytes, s.down_quant)
+    want, scale = _oracle_down(L, slots, midq)
+    hptrs = oracle.host_ptrs([L.host_slot(int(e)) for e in slots.reshape(-1)])
+    sw_d = down(slot_w)
+    want_b = oracle.moe_down_bias(want, hptrs, sw_d, s.hidden, n_slots, 1)
+    # the bias terms join the condition scale: sum_s |w_s * down_b_s|
+    for j in range(n_slots):
+        scale[0] += np.abs(sw_d[0, j] * L.bank.down_b[int(slots[0, j])].astype(np.float64))
+    _check(s.name + "/down_biased", down(out), want_b, scale, False)
