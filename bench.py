@@ -1,34 +1,51 @@
 """Benchmark of the quantized expert-matvec hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...] [--no-cpu]
+                    [--pmc-run WORKLOAD]
 
-Prints ONE JSON line. The headline (`value`) is BASELINE config 2's decode
-matvec: Q6_K 8192 x 4096 against one q8_K token, as algorithmic HBM GB/s
-(weight bytes + activation bytes + output bytes, per launch, / time). Every
-other configuration is reported under "results":
+Prints ONE JSON line. The headline (`value`) is the largest single-GPU
+configuration: a routed-MoE chunk layer of 16 tokens,
+hidden 4096, 128 Q2_K experts of FFN 1536, top-8 by a softmax router, run
+through the grouped path (router_logits_q8 -> moe_route_group -> grouped
+gate/up -> quantize -> grouped down -> slot sum). `value` is that layer's
+algorithmic HBM GB/s: the weight bytes of the distinct experts it touches
+(each once), the router weights and the activations in and out, divided by
+the layer time. A step is one layer; exactly K steps are timed. `roofline`
+is the layer's dominant kernel, the grouped gate/up stage
+(moe_grouped_mmq_kq_kernel<0, true>), timed on its own with HIP events over
+K launches on pre-routed chunks. Every other configuration is reported
+under "results":
   c1  Q4_K 4096x4096 matvec, batch 1
-  c2  Q6_K 8192x4096 matvec, batch 1 (headline) and 16-token chunk
+  c2  Q6_K 8192x4096 matvec, batch 1 and 16-token chunk
   c3  routed-MoE decode layer (Q4_K gate/up, Q6_K down, top-8 of 256 + shared)
-  c4  routed-MoE 16-token chunk layer (Q2_K and IQ2_XXS, top-8 of 128, grouped)
+  c4  the headline, and the same layer with IQ2_XXS experts
   c5  gpt-oss MXFP4 MoE layer (top-4 of 32, biases, swiglu_oai), batch 1 and 64
-A "step" is one pass of the path over one batch: one matvec launch (c1, c2)
-or one whole layer (c3-c5: router GEMV, top-k, device pointer build, q8_K
-quantize, gate/up/combine, mid quantize, down [+ grouping, bias]). Inputs are
-resident in HBM before the timed region; weights rotate over >= 2 GB of
-distinct copies / layer banks so the 256 MB Infinity Cache cannot serve them,
-and each layer step routes a different seeded token batch. Timing: HIP events
-on the per-thread default stream (the stream every pulsar_* launch uses) bracketing exactly
-K steps after W warm-up steps, with a device synchronize on both sides.
+Inputs are resident in HBM before the timed region; weights rotate over
+distinct device copies / layer banks (>= 2.2 GB) and each timed replay of the
+result configurations covers at least 2.2 GB of weights whatever --steps is
+(it times max(K, enough steps) and reports the time per step), so the 256 MB
+Infinity Cache cannot serve them; each layer step routes a different seeded
+token batch. Timing: HIP events on the per-thread default stream (the stream
+every pulsar_* launch uses) around the steps, eagerly and as one HIP-graph
+replay captured on that stream (the reference decodes from CUDA graphs,
+crates/kernels/src/lib.rs:755-811); the graph figure is the reported one.
 
 cpu_baseline: the oracle's C restatement of the reference CPU lane
-(oracle/pulsar_oracle.c) timed on this host's cores on a bounded sample of the
-headline workload; it is a reported baseline, not the target.
+(oracle/pulsar_oracle.c, AVX2 dots bit-identical to the scalar ones, the
+Lane's job split) timed on this host's cores on a bounded sample of the
+headline workload; a reported baseline, not the target.
+
+--pmc-run WORKLOAD runs only a workload for the `rocprofv3 --pmc` passes
+(no timing, no JSON): ten eager steps of c2_chunk16, c3, c4_q2k,
+c4_iq2xxs or c5_b64 ("all" runs each), then five copies of a 256 MiB device
+buffer that calibrate FETCH_SIZE / WRITE_SIZE.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -42,26 +59,27 @@ METRIC = "expert matvec HBM GB/s (% of peak); routed-MoE layer µs/token, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 ROTATE_BYTES = 2_200_000_000
-HEADLINE = "c2_q6k_8192x4096_decode"
+HEADLINE = "c4_moe_chunk16_q2k"
+ROOF_KERNEL = "pk::moe_grouped_mmq_kq_kernel<0u, true>"
 
 
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", nargs="*", default=None, help="subset of result names")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--pmc-run", action="store_true",
-                    help="only the workload of the rocprofv3 --pmc traffic passes (no timing, no JSON)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-run", default=None,
+                    help="only the workload of the rocprofv3 --pmc passes (no timing, no JSON)")
     return ap.parse_args()
 
 
 class Timer:
     """HIP events on the launch stream (the per-thread default stream every
-    pulsar_* launch uses) around K steps, two ways: eager launches from
-    Python, and one replay of a HIP graph holding the same K steps, captured
+    pulsar_* launch uses) around n steps, two ways: eager launches from
+    Python, and one replay of a HIP graph holding the same n steps, captured
     on that stream as the reference's decode graphs are
     (crates/kernels/src/lib.rs:755-811)."""
 
@@ -106,6 +124,12 @@ def dev_copies(torch, host: np.ndarray, min_total: int, slack: int = 256):
     return buf
 
 
+def covering_steps(steps: int, bytes_per_step: float) -> int:
+    """Steps per timed replay: at least `steps`, and enough that the replay
+    reads >= ROTATE_BYTES of distinct weights."""
+    return max(steps, int(-(-ROTATE_BYTES // max(1.0, bytes_per_step))))
+
+
 # ----------------------------------------------------------------- matvec --
 
 def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
@@ -123,7 +147,8 @@ def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
     def step(i):
         K.matmul_kq(out, ptrs[i % n], xq, cols, rows, n_tok, rb, quant)
 
-    tm = ctx["timer"].run(step, steps, warmup)
+    launches = max(steps, n)  # every copy once per replay
+    tm = ctx["timer"].run(step, launches, warmup)
     ms = tm["ms"]
     alg = w.nbytes + xq.numel() + out.numel() * 4
     res = {
@@ -134,13 +159,15 @@ def bench_matvec(ctx, name, quant, rows, cols, n_tok, steps, warmup):
         "us_per_launch_eager": tm["ms_eager"] * 1e3,
         "GBps": alg / (ms * 1e-3) / 1e9,
         "rotation_copies": n,
+        "launches_per_replay": launches,
+        "weight_bytes_per_replay": launches * w.nbytes,
     }
     res["pct_of_peak"] = 100 * res["GBps"] / HBM_PEAK_GBS
     if n_tok > 1:
         res["int_ops"] = 2 * rows * cols * n_tok
         # int8 MFMA roofline: dense 5.0 POP/s on MI355X
         res["TOPS"] = res["int_ops"] / (ms * 1e-3) / 1e12
-        res["mfma_frac"] = res["TOPS"] / INT8_PEAK_TOPS
+        res["mfma_frac_time_derived"] = res["TOPS"] / INT8_PEAK_TOPS
     del copies
     return res
 
@@ -154,16 +181,13 @@ class DevLayer:
         torch, synth = ctx["torch"], ctx["synth"]
         bank = synth.moe_bank(spec, seed=21)
         self.spec, self.host = spec, bank
-        E = spec.n_expert
         gsz, dsz = spec.ffn * spec.gate_row_bytes, spec.hidden * spec.down_row_bytes
         self.gsz, self.dsz = gsz, dsz
         self.banks = []
         for _ in range(n_banks):
-            g = dev_copies(torch, bank.gate, 0)
-            u = dev_copies(torch, bank.up, 0)
-            d = dev_copies(torch, bank.down, 0)
-            b = {"gate": g, "up": u, "down": d}
-            b["router_w"] = torch.from_numpy(bank.router_w).cuda()
+            b = {"gate": dev_copies(torch, bank.gate, 0), "up": dev_copies(torch, bank.up, 0),
+                 "down": dev_copies(torch, bank.down, 0),
+                 "router_w": torch.from_numpy(bank.router_w).cuda()}
             for k in ("router_b", "gate_b", "up_b", "down_b"):
                 a = getattr(bank, k)
                 b[k] = None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
@@ -182,16 +206,122 @@ class DevLayer:
         )
 
 
-def bench_moe(ctx, spec, steps, warmup, path: str):
-    """One whole layer per step. path: "plain" (reference entry points with
-    device routing), "grouped" (router_logits_q8 + moe_route_group + the
-    grouped stages + moe_slot_sum[_bias]: six launches), "grouped_split"
-    (the same grouped stages behind the reference's separate router, select,
-    pointer and CSR entry points: nine or ten), "fused" (router_logits_q8 +
+class LayerBufs:
+    """Activations and per-step routing buffers of one layer configuration."""
+
+    def __init__(self, ctx, s, n_sel: int, n_x: int):
+        torch, fm, synth = ctx["torch"], ctx["fm"], ctx["synth"]
+        f32 = dict(dtype=torch.float32, device="cuda")
+        u8 = dict(dtype=torch.uint8, device="cuda")
+        xs = synth.activations(n_x * s.n_tok, s.hidden, synth.rng_for(31, s.name))
+        self.xs = torch.from_numpy(xs).cuda().view(n_x, s.n_tok, s.hidden)
+        self.n_x = n_x
+        self.n_slots = n_slots = s.n_slots
+        self.nb_in, self.nb_mid = fm.q8k_blocks(s.hidden), fm.q8k_blocks(s.ffn)
+        self.logits = torch.zeros((s.n_tok, s.n_expert), **f32)
+        self.zero_bias = torch.zeros(s.n_expert, **f32)
+        self.sel_all = torch.zeros((n_sel, s.n_tok, s.k_used), dtype=torch.int32, device="cuda")
+        self.rw = torch.zeros((s.n_tok, s.k_used), **f32)
+        self.ptrs = torch.zeros(s.n_tok * n_slots * 48, **u8)
+        self.slot_w = torch.zeros((s.n_tok, n_slots), **f32)
+        self.xq = torch.zeros(s.n_tok * self.nb_in * 292, **u8)
+        self.mid = torch.zeros((s.n_tok * n_slots, s.ffn), **f32)
+        self.midq = torch.zeros(s.n_tok * n_slots * self.nb_mid * 292, **u8)
+        self.out = torch.zeros((s.n_tok, s.hidden), **f32)
+        self.max_groups = min(s.n_expert, s.n_tok * n_slots)
+        self.gptrs = torch.zeros(self.max_groups * 48, **u8)
+        self.starts = torch.zeros(self.max_groups + 1, dtype=torch.int32, device="cuda")
+        self.pairs = torch.zeros(s.n_tok * n_slots, dtype=torch.int32, device="cuda")
+        self.partial = torch.zeros((s.n_tok * n_slots, s.hidden), **f32)
+
+
+def layer_step(ctx, s, L, B, descs, shared, path):
+    """One layer per call. path: "plain" (reference entry points with device
+    routing), "grouped" (router_logits_q8 + moe_route_group + the grouped
+    stages + moe_slot_sum[_bias]: six launches), "grouped_split" (the same
+    grouped stages behind the reference's separate router, select, pointer and
+    CSR entry points: nine or ten), "fused" (router_logits_q8 +
     moe_pair_routed + moe_down_f32: three launches) or "fused_q"
     (router_logits_q8 + moe_pair_routed + quantize_q8_k + moe_down_biased:
     four; for wide mid rows, where every fused-down block re-quantizing the
     token's whole mid costs more than one quantize launch)."""
+    K = ctx["K"]
+    n_banks = len(L.banks)
+    n_slots = B.n_slots
+
+    def step(i):
+        b = L.banks[i % n_banks]
+        desc = descs[i % n_banks]
+        sh = shared[i % n_banks] if shared else None
+        x = B.xs[i % B.n_x]
+        sel = B.sel_all[i % B.sel_all.shape[0]]
+        if path in ("fused", "fused_q"):
+            K.router_logits_q8(B.logits, B.xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+            K.moe_pair_routed(B.mid, B.ptrs, B.slot_w, sel, B.rw, B.logits, None, s.n_expert, s.k_used, 1.0, 1,
+                              desc, sh, B.xq, s.hidden, s.ffn, s.n_tok, s.gate_row_bytes, s.gate_quant, s.act_op)
+            if path == "fused":
+                K.moe_down_f32(B.out, B.ptrs, B.slot_w, B.mid, s.ffn, s.hidden, n_slots, s.n_tok,
+                               s.down_row_bytes, s.down_quant, s.biases)
+            else:
+                K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+                K.moe_down_biased(B.out, B.ptrs, B.slot_w, B.midq, s.ffn, s.hidden, n_slots, s.n_tok,
+                                  s.down_row_bytes, s.down_quant)
+            return
+        if path == "grouped":
+            K.router_logits_q8(B.logits, B.xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+            K.moe_route_group(sel, B.rw, B.ptrs, B.slot_w, B.gptrs, B.starts, B.pairs, B.logits, None, s.n_expert,
+                              s.k_used, 1.0, 1, desc, sh, s.n_tok, B.max_groups)
+            K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, n_slots,
+                                      B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+            K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, n_slots,
+                               B.max_groups, s.down_row_bytes, s.down_quant)
+            if s.biases:
+                K.moe_slot_sum_bias(B.out, B.partial, B.ptrs, B.slot_w, s.hidden, n_slots, s.n_tok)
+            else:
+                K.moe_slot_sum(B.out, B.partial, s.hidden, n_slots, s.n_tok)
+            return
+        K.matmul_f32(B.logits, b["router_w"], x, s.hidden, s.n_expert, s.n_tok)
+        if b["router_b"] is not None:
+            K.add_bias_rows(B.logits, b["router_b"], s.n_expert, s.n_tok)
+        K.router_select(sel, B.rw, B.logits, B.zero_bias, s.n_expert, s.k_used, 1.0, s.n_tok, 1, 0)
+        K.moe_route_ptrs(B.ptrs, B.slot_w, sel, B.rw, desc, s.n_expert, sh, s.n_tok, s.k_used)
+        K.quantize_q8_k(B.xq, x, s.hidden, s.n_tok)
+        if path == "grouped_split":
+            K.moe_group_csr(B.gptrs, B.starts, B.pairs, B.ptrs, s.n_tok, n_slots, B.max_groups)
+            K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, n_slots,
+                                      B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+            K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, n_slots,
+                               B.max_groups, s.down_row_bytes, s.down_quant)
+            K.moe_slot_sum(B.out, B.partial, s.hidden, n_slots, s.n_tok)
+        else:
+            K.moe_pair_swiglu(B.mid, B.ptrs, B.slot_w, B.xq, s.hidden, s.ffn, n_slots, s.n_tok, s.gate_row_bytes,
+                              s.gate_quant, s.act_op)
+            K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            K.moe_down(B.out, B.ptrs, B.midq, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes, s.down_quant)
+        if s.biases:
+            K.moe_down_bias(B.out, B.ptrs, B.slot_w, s.hidden, n_slots, s.n_tok)
+
+    return step
+
+
+def layer_alg_bytes(s, fm, distinct: float) -> float:
+    """Algorithmic bytes of one layer: each distinct expert's weights (and
+    biases) once, the router weights, x in (f32, then its q8_K), out."""
+    nb_in = fm.q8k_blocks(s.hidden)
+    bias_bytes = 4 * (2 * s.ffn + s.hidden) if s.biases else 0
+    act_bytes = s.n_tok * s.hidden * 4 * 2 + s.n_tok * nb_in * 292
+    router_bytes = s.n_expert * s.hidden * 4 + (s.n_expert * 4 if s.biases else 0)
+    return distinct * (s.expert_bytes + bias_bytes) + router_bytes + act_bytes
+
+
+def expected_distinct(s) -> float:
+    """E[distinct experts] of a chunk whose tokens each pick k of E uniformly."""
+    return s.n_expert * (1 - (1 - s.k_used / s.n_expert) ** s.n_tok) + (1 if s.shared else 0)
+
+
+def bench_moe(ctx, spec, steps, warmup, path: str, exact_steps: bool = False, stage_timing: bool = False):
     torch, K, fm = ctx["torch"], ctx["K"], ctx["fm"]
     s = spec
     bank_bytes = s.n_expert * s.expert_bytes
@@ -199,90 +329,15 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
     L = DevLayer(ctx, spec, n_banks)
     descs = [L.bank_desc(K, b) for b in L.banks]
     shared = [[tuple(t.data_ptr() for t in b["sh"])] for b in L.banks] if s.shared else None
-    n_x = 16  # distinct seeded token batches, one per step in rotation
-    xs = torch.from_numpy(ctx["synth"].activations(n_x * s.n_tok, s.hidden, ctx["synth"].rng_for(31, s.name))).cuda()
-    xs = xs.view(n_x, s.n_tok, s.hidden)
-    n_slots = s.n_slots
-    nb_in, nb_mid = fm.q8k_blocks(s.hidden), fm.q8k_blocks(s.ffn)
-    f32 = dict(dtype=torch.float32, device="cuda")
-    logits = torch.zeros((s.n_tok, s.n_expert), **f32)
-    zero_bias = torch.zeros(s.n_expert, **f32)
-    sel_all = torch.zeros((steps + warmup, s.n_tok, s.k_used), dtype=torch.int32, device="cuda")
-    rw = torch.zeros((s.n_tok, s.k_used), **f32)
-    ptrs = torch.zeros(s.n_tok * n_slots * 48, dtype=torch.uint8, device="cuda")
-    slot_w = torch.zeros((s.n_tok, n_slots), **f32)
-    xq = torch.zeros(s.n_tok * nb_in * 292, dtype=torch.uint8, device="cuda")
-    mid = torch.zeros((s.n_tok * n_slots, s.ffn), **f32)
-    midq = torch.zeros(s.n_tok * n_slots * nb_mid * 292, dtype=torch.uint8, device="cuda")
-    out = torch.zeros((s.n_tok, s.hidden), **f32)
-    max_groups = min(s.n_expert, s.n_tok * n_slots)
-    gptrs = torch.zeros(max_groups * 48, dtype=torch.uint8, device="cuda")
-    starts = torch.zeros(max_groups + 1, dtype=torch.int32, device="cuda")
-    pairs = torch.zeros(s.n_tok * n_slots, dtype=torch.int32, device="cuda")
-    partial = torch.zeros((s.n_tok * n_slots, s.hidden), **f32)
-
-    def step(i):
-        b = L.banks[i % n_banks]
-        x = xs[i % n_x]
-        sel = sel_all[i]
-        if path in ("fused", "fused_q"):
-            K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
-            K.moe_pair_routed(mid, ptrs, slot_w, sel, rw, logits, None, s.n_expert, s.k_used, 1.0, 1,
-                              descs[i % n_banks], shared[i % n_banks] if shared else None, xq, s.hidden, s.ffn,
-                              s.n_tok, s.gate_row_bytes, s.gate_quant, s.act_op)
-            if path == "fused":
-                K.moe_down_f32(out, ptrs, slot_w, mid, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
-                               s.down_quant, s.biases)
-            else:
-                K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
-                K.moe_down_biased(out, ptrs, slot_w, midq, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes,
-                                  s.down_quant)
-            return
-        if path == "grouped":
-            K.router_logits_q8(logits, xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
-            K.moe_route_group(sel, rw, ptrs, slot_w, gptrs, starts, pairs, logits, None, s.n_expert, s.k_used, 1.0,
-                              1, descs[i % n_banks], shared[i % n_banks] if shared else None, s.n_tok, max_groups)
-            K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq, s.hidden, s.ffn, n_slots,
-                                      max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
-            K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
-            K.moe_down_grouped(partial, gptrs, starts, pairs, midq, s.ffn, s.hidden, n_slots, max_groups,
-                               s.down_row_bytes, s.down_quant)
-            if s.biases:
-                K.moe_slot_sum_bias(out, partial, ptrs, slot_w, s.hidden, n_slots, s.n_tok)
-            else:
-                K.moe_slot_sum(out, partial, s.hidden, n_slots, s.n_tok)
-            return
-        K.matmul_f32(logits, b["router_w"], x, s.hidden, s.n_expert, s.n_tok)
-        if b["router_b"] is not None:
-            K.add_bias_rows(logits, b["router_b"], s.n_expert, s.n_tok)
-        K.router_select(sel, rw, logits, zero_bias, s.n_expert, s.k_used, 1.0, s.n_tok, 1, 0)
-        K.moe_route_ptrs(ptrs, slot_w, sel, rw, descs[i % n_banks], s.n_expert,
-                         shared[i % n_banks] if shared else None, s.n_tok, s.k_used)
-        K.quantize_q8_k(xq, x, s.hidden, s.n_tok)
-        if path == "grouped_split":
-            K.moe_group_csr(gptrs, starts, pairs, ptrs, s.n_tok, n_slots, max_groups)
-            K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, slot_w, xq, s.hidden, s.ffn, n_slots,
-                                      max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
-            K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
-            K.moe_down_grouped(partial, gptrs, starts, pairs, midq, s.ffn, s.hidden, n_slots, max_groups,
-                               s.down_row_bytes, s.down_quant)
-            K.moe_slot_sum(out, partial, s.hidden, n_slots, s.n_tok)
-        else:
-            K.moe_pair_swiglu(mid, ptrs, slot_w, xq, s.hidden, s.ffn, n_slots, s.n_tok, s.gate_row_bytes,
-                              s.gate_quant, s.act_op)
-            K.quantize_q8_k(midq, mid, s.ffn, s.n_tok * n_slots)
-            K.moe_down(out, ptrs, midq, s.ffn, s.hidden, n_slots, s.n_tok, s.down_row_bytes, s.down_quant)
-        if s.biases:
-            K.moe_down_bias(out, ptrs, slot_w, s.hidden, n_slots, s.n_tok)
-
-    tm = ctx["timer"].run(step, steps, warmup)
+    est = layer_alg_bytes(s, fm, expected_distinct(s))
+    n = steps if exact_steps else covering_steps(steps, est)
+    B = LayerBufs(ctx, s, n + warmup, n_x=64)
+    step = layer_step(ctx, s, L, B, descs, shared, path)
+    tm = ctx["timer"].run(step, n, warmup)
     ms = tm["ms"]
-    sel_h = sel_all[warmup:].cpu().numpy()
-    distinct = np.array([len(np.unique(sel_h[i])) for i in range(steps)]) + (1 if s.shared else 0)
-    bias_bytes = 4 * (2 * s.ffn + s.hidden) if s.biases else 0
-    act_bytes = s.n_tok * s.hidden * 4 * 2 + s.n_tok * nb_in * 292
-    router_bytes = s.n_expert * s.hidden * 4 + (s.n_expert * 4 if s.biases else 0)
-    alg = float(np.mean(distinct)) * (s.expert_bytes + bias_bytes) + router_bytes + act_bytes
+    sel_h = B.sel_all[warmup:warmup + n].cpu().numpy()
+    distinct = np.array([len(np.unique(sel_h[i])) for i in range(n)]) + (1 if s.shared else 0)
+    alg = layer_alg_bytes(s, fm, float(np.mean(distinct)))
     res = {
         "path": path,
         "n_tok": s.n_tok,
@@ -293,101 +348,239 @@ def bench_moe(ctx, spec, steps, warmup, path: str):
         "alg_bytes": alg,
         "GBps": alg / (ms * 1e-3) / 1e9,
         "layer_banks": n_banks,
+        "layers_per_replay": n,
     }
     res["pct_of_peak"] = 100 * res["GBps"] / HBM_PEAK_GBS
-    del L
+    if stage_timing:
+        res["stages"] = grouped_stage_timing(ctx, s, L, descs, shared, steps, warmup)
+    del L, B
     torch.cuda.empty_cache()
     return res
 
 
-def stream_peak(ctx) -> float:
+def grouped_stage_timing(ctx, s, L, descs, shared, steps, warmup):
+    """The grouped gate/up and down stages timed alone: `steps` launches of
+    each over chunks routed beforehand (one routing per bank and token batch,
+    so consecutive launches read different experts of different banks), HIP
+    events around a graph replay of the launches. Algorithmic bytes per
+    launch: the gate and up (down) matrices of every distinct expert of the
+    chunk once, each pair's activation row in (q8_K), its output row out."""
+    torch, K, fm = ctx["torch"], ctx["K"], ctx["fm"]
+    n_banks = len(L.banks)
+    n_route = max(2 * n_banks, 8)
+    Bs = [LayerBufs(ctx, s, 1, n_x=1) for _ in range(n_route)]
+    xs = ctx["synth"].activations(n_route * s.n_tok, s.hidden, ctx["synth"].rng_for(47, s.name))
+    xs = torch.from_numpy(xs).cuda().view(n_route, s.n_tok, s.hidden)
+    distinct = []
+    for i, B in enumerate(Bs):
+        b = L.banks[i % n_banks]
+        K.router_logits_q8(B.logits, B.xq, xs[i], b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+        K.moe_route_group(B.sel_all[0], B.rw, B.ptrs, B.slot_w, B.gptrs, B.starts, B.pairs, B.logits, None,
+                          s.n_expert, s.k_used, 1.0, 1, descs[i % n_banks], shared[i % n_banks] if shared else None,
+                          s.n_tok, B.max_groups)
+        K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, B.n_slots,
+                                  B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+        K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * B.n_slots)
+        st = B.starts.cpu().numpy()
+        distinct.append(int(np.count_nonzero(np.diff(st))))
+    d = float(np.mean(distinct))
+    n_pairs = s.n_tok * s.n_slots
+    nb_in, nb_mid = fm.q8k_blocks(s.hidden), fm.q8k_blocks(s.ffn)
+    out = {}
+
+    def pair(i):
+        B = Bs[i % n_route]
+        K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, B.n_slots,
+                                  B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+
+    def down(i):
+        B = Bs[i % n_route]
+        K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, B.n_slots,
+                           B.max_groups, s.down_row_bytes, s.down_quant)
+
+    q = s.gate_quant
+    stages = (("gate_up", pair, f"pk::moe_grouped_mmq_kq_kernel<{q}u, true>",
+               d * 2 * s.ffn * s.gate_row_bytes + n_pairs * nb_in * 292 + n_pairs * s.ffn * 4),
+              ("down", down, f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false>",
+               d * s.hidden * s.down_row_bytes + n_pairs * nb_mid * 292 + n_pairs * s.hidden * 4))
+    for name, fn, kernel, alg in stages:
+        tm = ctx["timer"].run(fn, max(steps, n_route), warmup)
+        us = tm["ms"] * 1e3
+        out[name] = {"kernel": kernel, "alg_bytes_per_launch": alg, "us_per_launch": us,
+                     "us_per_launch_eager": tm["ms_eager"] * 1e3, "GBps": alg / (us * 1e-6) / 1e9,
+                     "launches_timed": max(steps, n_route), "mean_distinct_experts": d}
+        out[name]["frac"] = out[name]["GBps"] / HBM_PEAK_GBS
+    del Bs
+    return out
+
+
+def stream_ceiling(ctx, nbytes: int, reps: int = 10) -> float:
+    """GB/s of the streaming-read probe (pulsar_bw_read) over `nbytes`
+    regions, rotating so consecutive launches read different memory."""
     torch, K = ctx["torch"], ctx["K"]
-    nbytes = 4 << 30
-    buf = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    nbytes = max(256, nbytes // 256 * 256)  # whole 16-byte loads, regions 256-byte aligned
+    n_reg = max(2, -(-ROTATE_BYTES // nbytes)) if nbytes < ROTATE_BYTES else 1
+    buf = torch.ones(n_reg * nbytes // 4, dtype=torch.float32, device="cuda")
     sink = torch.zeros(4, dtype=torch.float32, device="cuda")
-    ms = ctx["timer"].run(lambda i: K.bw_read(buf, nbytes, sink), 10, 3)["ms"]
+    base = buf.data_ptr()
+    ms = ctx["timer"].run(lambda i: K.bw_read(base + (i % n_reg) * nbytes, nbytes, sink), max(reps, n_reg), 3)["ms"]
     del buf
     return nbytes / (ms * 1e-3) / 1e9
 
 
 # ------------------------------------------------------------ CPU baseline --
 
-def cpu_baseline(seconds: float) -> dict:
-    """The oracle's threaded lane restatement on the headline workload
-    (Q6_K 8192 x 4096 decode), rotating over >= 1 GB of host copies so the
-    working set exceeds the last-level cache. Q6_K is not a lane format in
-    the reference (crates/engine/src/lib.rs:2103-2114): this is a
-    restatement of lane semantics."""
-    import oracle
-    from pulsar_amd import synth
-    from pulsar_amd.formats import QUANT_Q6_K, row_bytes
+def cpu_info() -> dict:
+    info = {"model": "unknown", "physical_cores": None, "logical_cpus": os.cpu_count()}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {k.strip(): v.strip() for k, v in (ln.split(":", 1) for ln in txt.splitlines() if ":" in ln)}
+        info["model"] = kv.get("Model name", info["model"])
+        if "Core(s) per socket" in kv and "Socket(s)" in kv:
+            info["physical_cores"] = int(kv["Core(s) per socket"]) * int(kv["Socket(s)"])
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if info["model"] == "unknown":
+        try:
+            with open("/proc/cpuinfo") as f:
+                info["model"] = next(ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
+    return info
 
-    rows, cols = 8192, 4096
-    w = synth.quant_matrix(QUANT_Q6_K, rows, cols, synth.rng_for(11, HEADLINE))
-    n_copies = max(1, -(-1_000_000_000 // w.nbytes))
-    copies = [w.copy() for _ in range(n_copies)]
-    x = synth.activations(1, cols, synth.rng_for(12, HEADLINE))
-    xq = oracle.quantize_q8_k(x)
-    out = np.zeros((1, rows), np.float32)
-    # this process's CPU share (16 threads on the GPU boxes, whatever nproc says)
-    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(16, avail))
-    lane_threads = max(1, threads // 2 - 2)  # the lane's default pool, (logical / 2) - 2 (elib:1896)
-    rb = row_bytes(QUANT_Q6_K, cols)
-    alg = w.nbytes + xq.nbytes + out.nbytes
+
+def cpu_baseline(seconds: float, ctx) -> dict:
+    """The oracle's threaded restatement of the reference CPU lane
+    (po_lane_moe: per token q8_K quantize, gate/up/GLU jobs over 256-row
+    chunks, mid quantize, down jobs over 512-row chunks, crates/engine/src/
+    lib.rs:1994-2100; AVX2 Q2_K dots, cpu_dot.rs:626-671) on the headline
+    layer: config 4, 16 tokens routed top-8 of 128 Q2_K experts, each layer a
+    different seeded token batch over one 793 MB host bank (a layer touches
+    ~510 MB, far beyond the last-level cache). Timed at the lane's default
+    pool, (logical / 2) - 2 threads (elib:1896), and at this process's whole
+    CPU share. The reference lane takes at most 8 tokens (elib:7900-7908), so
+    a 16-token chunk is a restatement of lane semantics."""
+    import oracle
+
+    synth, fm = ctx["synth"], ctx["fm"]
+    s = synth.C4_Q2K
+    bank = synth.moe_bank(s, seed=21)
+    n_x = 8
+    xs = synth.activations(n_x * s.n_tok, s.hidden, synth.rng_for(31, s.name)).reshape(n_x, s.n_tok, s.hidden)
+    routed = []
+    for i in range(n_x):
+        lg = oracle.matmul_f32(bank.router_w, xs[i], s.hidden, s.n_expert, s.n_tok)
+        sel, rw = oracle.router_select(lg, None, s.n_expert, s.k_used, 1.0, s.n_tok, 1, 0)
+        ptrs = oracle.host_ptrs([(bank.gate[e], bank.up[e], bank.down[e]) for e in sel.reshape(-1)])
+        routed.append((ptrs, rw, np.ascontiguousarray(xs[i]), len(np.unique(sel))))
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(16, avail))  # this process's CPU share (16 on the GPU boxes)
+    lane_threads = max(1, threads // 2 - 2)
+    prev = oracle.set_simd(True)
 
     def timed(nt, budget):
-        oracle.matmul_kq_mt(copies[0], xq, cols, rows, 1, rb, QUANT_Q6_K, nt, out)  # warm the pool
-        t0 = time.perf_counter()
-        n = 0
-        while time.perf_counter() - t0 < budget:
-            oracle.matmul_kq_mt(copies[n % n_copies], xq, cols, rows, 1, rb, QUANT_Q6_K, nt, out)
+        oracle.lane_moe(*routed[0][:3], s.hidden, s.ffn, s.hidden, s.k_used, s.n_tok, s.gate_row_bytes,
+                        s.gate_quant, s.down_row_bytes, s.down_quant, s.act_op, nt)  # warm the pool
+        t0, n, d = time.perf_counter(), 0, 0
+        while time.perf_counter() - t0 < budget or n == 0:
+            ptrs, rw, x, nd = routed[n % n_x]
+            oracle.lane_moe(ptrs, rw, x, s.hidden, s.ffn, s.hidden, s.k_used, s.n_tok, s.gate_row_bytes,
+                            s.gate_quant, s.down_row_bytes, s.down_quant, s.act_op, nt)
             n += 1
-        return n, time.perf_counter() - t0
+            d += nd
+        dt = time.perf_counter() - t0
+        alg = layer_alg_bytes(s, fm, d / n)
+        return {"threads": nt, "layers": n, "seconds": round(dt, 2), "us_per_layer": dt / n * 1e6,
+                "value": alg / (dt / n) / 1e9, "unit": "GB/s"}
 
-    n, dt = timed(threads, seconds * 0.6)
-    n_l, dt_l = timed(lane_threads, seconds * 0.4)
-    model = "unknown"
     try:
-        with open("/proc/cpuinfo") as f:
-            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
+        full = timed(threads, seconds * 0.55)
+        lane = timed(lane_threads, seconds * 0.45)
+    finally:
+        oracle.set_simd(prev)
+    info = cpu_info()
     return {
-        "value": alg * n / dt / 1e9,
+        "value": full["value"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} passes of the Q6_K 8192x4096 decode matvec in {dt:.1f} s, {threads} threads, "
-                  f"{n_copies} rotating host copies ({n_copies * w.nbytes / 1e9:.1f} GB)",
-        "us_per_pass": dt / n * 1e6,
-        "lane_default": {"threads": lane_threads, "value": alg * n_l / dt_l / 1e9, "unit": "GB/s",
-                         "us_per_pass": dt_l / n_l * 1e6},
-        "cpu_model": model,
-        "logical_cpus_visible": os.cpu_count(),
+        "sample": f"{full['layers']} config-4 Q2_K layers (16 tokens, top-8 of 128) on the AVX2 lane "
+                  f"restatement in {full['seconds']} s with {threads} threads; 793 MB host bank, "
+                  f"{n_x} token batches in rotation; expert FFN only (router on the GPU in the reference)",
+        "us_per_layer": full["us_per_layer"],
+        "avx2": oracle.avx2_supported(),
+        "lane_default": lane,
+        "cpu_model": info["model"],
+        "physical_cores": info["physical_cores"],
+        "logical_cpus_visible": info["logical_cpus"],
+        "threads_available": avail,
     }
 
 
-def pmc_run(ctx):
-    """Workload of the `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
-    passes: 20 eager launches each of the c2 decode matvec and the c2
-    16-token MFMA matvec over rotating weight copies, then five copies of a
-    256 MiB device buffer (reads 256 MiB, writes 256 MiB: the calibration of
-    both counters)."""
+# --------------------------------------------------------------- PMC runs --
+
+def pmc_run(ctx, which: str):
+    """Workloads of the rocprofv3 --pmc passes: ten eager steps of each named
+    configuration on rotating weights, then five copies of a 256 MiB device
+    buffer (reads 256 MiB, writes 256 MiB: the calibration of FETCH_SIZE and
+    WRITE_SIZE). Prints one `pmc-alg {json}` line per configuration with the
+    algorithmic bytes per dispatch of its main kernels, the figures the
+    counters are compared with."""
     torch, K, synth, fm = ctx["torch"], ctx["K"], ctx["synth"], ctx["fm"]
-    q, rows, cols = fm.QUANT_Q6_K, 8192, 4096
-    w = synth.quant_matrix(q, rows, cols, synth.rng_for(11, "pmc"))
-    copies = dev_copies(torch, w, 1_000_000_000)
-    rb = fm.row_bytes(q, cols)
-    for n_tok in (1, 16):
-        x = torch.from_numpy(synth.activations(n_tok, cols, synth.rng_for(12, "pmc"))).cuda()
-        xq = torch.zeros(n_tok * fm.q8k_blocks(cols) * 292, dtype=torch.uint8, device="cuda")
-        K.quantize_q8_k(xq, x, cols, n_tok)
-        out = torch.zeros((n_tok, rows), dtype=torch.float32, device="cuda")
-        for i in range(20):
-            K.matmul_kq(out, copies[i % copies.shape[0]], xq, cols, rows, n_tok, rb, q)
+    names = ["c2_chunk16", "c3", "c4_q2k", "c4_iq2xxs", "c5_b64"] if which == "all" else which.split(",")
+    specs = {"c3": (synth.C3, "fused"), "c4_q2k": (synth.C4_Q2K, "grouped"),
+             "c4_iq2xxs": (synth.C4_IQ2, "grouped"), "c5_b64": (synth.C5_B64, "grouped")}
+    for name in names:
+        print(f"pmc-run {name}", flush=True)
+        if name == "c2_chunk16":
+            q, rows, cols = fm.QUANT_Q6_K, 8192, 4096
+            w = synth.quant_matrix(q, rows, cols, synth.rng_for(11, "pmc"))
+            copies = dev_copies(torch, w, 1_000_000_000)
+            rb = fm.row_bytes(q, cols)
+            alg = {}
+            for n_tok, kern in ((1, "pk::matvec_kernel<4u, 1u, 1u, 1u, 6u>"), (16, "pk::mmq_gemm_kernel<4u, 2u, 4u, 1u>")):
+                x = torch.from_numpy(synth.activations(n_tok, cols, synth.rng_for(12, "pmc"))).cuda()
+                xq = torch.zeros(n_tok * fm.q8k_blocks(cols) * 292, dtype=torch.uint8, device="cuda")
+                K.quantize_q8_k(xq, x, cols, n_tok)
+                out = torch.zeros((n_tok, rows), dtype=torch.float32, device="cuda")
+                for i in range(20):
+                    K.matmul_kq(out, copies[i % copies.shape[0]], xq, cols, rows, n_tok, rb, q)
+                alg[kern] = w.nbytes + xq.numel() + out.numel() * 4
+            torch.cuda.synchronize()
+            del copies
+            print("pmc-alg " + json.dumps({"workload": name, "alg": alg}), flush=True)
+            continue
+        s, path = specs[name]
+        n_banks = max(4, -(-ROTATE_BYTES // (s.n_expert * s.expert_bytes)))
+        L = DevLayer(ctx, s, n_banks)
+        descs = [L.bank_desc(K, b) for b in L.banks]
+        shared = [[tuple(t.data_ptr() for t in b["sh"])] for b in L.banks] if s.shared else None
+        B = LayerBufs(ctx, s, 10, n_x=10)
+        step = layer_step(ctx, s, L, B, descs, shared, path)
+        for i in range(10):
+            step(i)
         torch.cuda.synchronize()
-    del copies
+        sel = B.sel_all.cpu().numpy()
+        d = float(np.mean([len(np.unique(sel[i])) for i in range(10)])) + (1 if s.shared else 0)
+        n_pairs = s.n_tok * s.n_slots
+        nb_in, nb_mid = fm.q8k_blocks(s.hidden), fm.q8k_blocks(s.ffn)
+        gu = d * 2 * s.ffn * s.gate_row_bytes + (d * 2 * s.ffn * 4 if s.biases else 0)
+        dn = d * s.hidden * s.down_row_bytes
+        router = s.n_expert * s.hidden * 4 + s.n_tok * s.hidden * 4 + s.n_tok * s.n_expert * 4 + s.n_tok * nb_in * 292
+        if path == "grouped":
+            alg = {f"pk::router_logits_q8_kernel<4u>": router,
+                   f"pk::moe_grouped_mmq_kq_kernel<{s.gate_quant}u, true>":
+                       gu + n_pairs * nb_in * 292 + n_pairs * s.ffn * 4,
+                   f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false>":
+                       dn + n_pairs * nb_mid * 292 + n_pairs * s.hidden * 4}
+        else:
+            alg = {"pk::router_logits_q8_kernel<1u>": router,
+                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, 4u, 0u, 1u>":
+                       gu + s.n_tok * nb_in * 292 + s.n_tok * s.n_expert * 4 + n_pairs * s.ffn * 4,
+                   f"pk::moe_down_f32_kernel<{s.down_quant}u, 1u, 0u>": dn + n_pairs * s.ffn * 4 + s.n_tok * s.hidden * 4}
+        print("pmc-alg " + json.dumps({"workload": name, "mean_distinct_experts": d, "alg": alg}), flush=True)
+        del L, B
+        torch.cuda.empty_cache()
     src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(5):
@@ -396,15 +589,24 @@ def pmc_run(ctx):
     print("pmc-run done", flush=True)
 
 
-def pmc_traffic(name: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
-    p = ROOT / "profiles" / "pmc_traffic.json"
+def pmc_summary(kernel: str):
+    """Per-dispatch counters of `kernel` from the committed rocprofv3 --pmc
+    summary (profiles/pmc_counters.json), if any."""
+    p = ROOT / "profiles" / "pmc_counters.json"
     if not p.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(name)
+        return json.loads(p.read_text()).get(kernel)
     except (ValueError, OSError):
         return None
+
+
+def rounded(v):
+    if isinstance(v, float):
+        return round(v, 4)
+    if isinstance(v, dict):
+        return {k: rounded(x) for k, x in v.items()}
+    return v
 
 
 def main():
@@ -423,7 +625,7 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     ctx = {"torch": torch, "K": K, "synth": synth, "fm": fm, "timer": Timer(torch, K)}
     if args.pmc_run:
-        pmc_run(ctx)
+        pmc_run(ctx, args.pmc_run)
         return
     steps, warmup = args.steps, args.warmup
     want = set(args.only) if args.only else None
@@ -433,61 +635,80 @@ def main():
 
     results = {}
     if on(HEADLINE):
-        results[HEADLINE] = bench_matvec(ctx, HEADLINE, fm.QUANT_Q6_K, 8192, 4096, 1, steps, warmup)
+        results[HEADLINE] = bench_moe(ctx, synth.C4_Q2K, steps, warmup, "grouped", exact_steps=True,
+                                      stage_timing=True)
     if on("c1_q4k_4096x4096_decode"):
         results["c1_q4k_4096x4096_decode"] = bench_matvec(ctx, "c1", fm.QUANT_Q4_K, 4096, 4096, 1, steps, warmup)
+    if on("c2_q6k_8192x4096_decode"):
+        results["c2_q6k_8192x4096_decode"] = bench_matvec(ctx, "c2_q6k_8192x4096_decode", fm.QUANT_Q6_K, 8192,
+                                                          4096, 1, steps, warmup)
     if on("c2_q6k_8192x4096_chunk16"):
         results["c2_q6k_8192x4096_chunk16"] = bench_matvec(ctx, "c2c", fm.QUANT_Q6_K, 8192, 4096, 16, steps,
                                                            warmup)
-    layer_steps = max(20, steps // 2)
-    for spec, path in ((synth.C3, "fused"), (synth.C4_Q2K, "grouped"), (synth.C4_IQ2, "grouped"),
-                       (synth.C5_B1, "fused_q"), (synth.C5_B64, "grouped")):
+    for spec, path in ((synth.C3, "fused"), (synth.C4_IQ2, "grouped"), (synth.C5_B1, "fused_q"),
+                       (synth.C5_B64, "grouped")):
         if on(spec.name):
-            results[spec.name] = bench_moe(ctx, spec, layer_steps, warmup, path)
+            results[spec.name] = bench_moe(ctx, spec, steps, warmup, path,
+                                           stage_timing=spec is synth.C4_IQ2 or spec is synth.C5_B64)
         # the same layer through the reference's own (unfused) entry points
         if path.startswith("fused") and on(spec.name + "_unfused"):
-            results[spec.name + "_unfused"] = bench_moe(ctx, spec, layer_steps, warmup, "plain")
-        if spec is synth.C4_Q2K and on(spec.name + "_split"):
-            results[spec.name + "_split"] = bench_moe(ctx, spec, layer_steps, warmup, "grouped_split")
-    peak = stream_peak(ctx) if want is None else None
+            results[spec.name + "_unfused"] = bench_moe(ctx, spec, steps, warmup, "plain")
+    if on(HEADLINE + "_split"):
+        results[HEADLINE + "_split"] = bench_moe(ctx, synth.C4_Q2K, steps, warmup, "grouped_split")
 
-    head = results.get(HEADLINE) or next(iter(results.values()))
-    head_name = HEADLINE if HEADLINE in results else next(iter(results))
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
-    achieved = head.get("GBps")
+    head = results.get(HEADLINE)
+    ceilings = None
+    if want is None and head:
+        roof = head["stages"]["gate_up"]
+        ceilings = {"stream_read_4GiB_GBps": stream_ceiling(ctx, 4 << 30),
+                    "stream_read_at_roofline_kernel_bytes_GBps": stream_ceiling(ctx, int(roof["alg_bytes_per_launch"])),
+                    "roofline_kernel_bytes": int(roof["alg_bytes_per_launch"])}
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, ctx)
+    if head is None:  # a subset run without the headline
+        name, head = next(iter(results.items()))
+        print(json.dumps({"metric": METRIC, "partial_run": name, "results": rounded(results)}))
+        return
+    roof = head["stages"]["gate_up"]
+    pmc = pmc_summary(ROOF_KERNEL) or {}
     line = {
         "metric": METRIC,
-        "value": round(achieved, 2),
+        "value": round(head["GBps"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": head.get("us_per_launch", head.get("us_per_layer", 0.0)) / 1e3,
+        "ms_per_step": head["us_per_layer"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded random blocks of the stated formats; no checkpoints)",
         "config": {
-            "workload": "Q6_K matvec 8192x4096, decode batch 1 (BASELINE configs[1]); weights rotate over "
-                        f"{head.get('rotation_copies', 0)} HBM copies",
-            "rows": 8192, "cols": 4096, "n_tok": 1, "format": "Q6_K", "activation": "q8_K",
+            "workload": "BASELINE configs[3]: routed-MoE chunk layer, 16 tokens, hidden 4096, 128 Q2_K experts "
+                        "of FFN 1536, top-8 softmax router, grouped path (6 launches); "
+                        f"{head['layer_banks']} rotating layer banks of 793 MB",
+            "us_per_layer": round(head["us_per_layer"], 3),
+            "us_per_token": round(head["us_per_token"], 3),
+            "mean_distinct_experts": head["mean_distinct_experts"],
+            "alg_bytes_per_layer": head["alg_bytes"],
+            "format": "Q2_K", "activation": "q8_K", "n_tok": 16,
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 2),
+            "achieved": round(roof["GBps"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": pmc_traffic(head_name),
-            "kernel": head.get("kernel"),
-            "alg_bytes_per_launch": head.get("alg_bytes"),
-            "us_per_launch": round(head.get("us_per_launch", 0.0), 3),
+            "frac": round(roof["GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": pmc.get("hbm_bytes_per_dispatch"),
+            "kernel": ROOF_KERNEL,
+            "alg_bytes_per_launch": round(roof["alg_bytes_per_launch"]),
+            "us_per_launch": round(roof["us_per_launch"], 3),
+            "traffic_over_alg": pmc.get("traffic_over_alg"),
+            "mfma_busy_frac": pmc.get("mfma_busy_frac"),
         },
-        "cpu_baseline": cpu,
-        "stream_read_peak_GBps": None if peak is None else round(peak, 1),
-        "results": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in results.items()},
+        "cpu_baseline": rounded(cpu),
+        "stream_ceilings": rounded(ceilings),
+        "results": rounded(results),
     }
     print(json.dumps(line))
 
