@@ -9,8 +9,12 @@
  *     (crates/kernels/cuda/pulsar_kernels.cu:25-29);
  *   - every pointer argument except the self-tests' is a DEVICE pointer the
  *     caller owns; the library allocates nothing on these paths;
- *   - launches are asynchronous on the calling thread's current default
- *     stream (the null stream); nothing here synchronises.
+ *   - launches are asynchronous on the calling thread's per-thread default
+ *     stream (hipStreamPerThread), the stream the reference's
+ *     --default-stream=per-thread build launches on
+ *     (crates/kernels/build.rs:42-48), so a thread-local graph capture begun
+ *     on it records them; pulsar_set_stream selects another stream. Nothing
+ *     here synchronises.
  *
  * Byte layouts are the GGUF/ggml ones (crates/gguf/src/lib.rs:145-180):
  *   Q2_K 84 B / 256, Q4_K 144 B / 256, Q6_K 210 B / 256, IQ2_XXS 66 B / 256,
@@ -96,7 +100,10 @@ _Static_assert(sizeof(pulsar_expert_ptrs) == 48, "pulsar_expert_ptrs is 48 bytes
 int pulsar_quantize_q8_K(void *out, const void *x, uint32_t in_dim, uint32_t n_rows);
 
 /* out[t][r] = sum_b dot(w row r block b, xq[t] block b), fp32 [n_tok][out_dim].
- * quant in {Q2_K, IQ2_XXS, Q4_K, Q6_K}; in_dim % 256 == 0.
+ * quant: the reference's dense list (pulsar_kernels.cu:5090-5142) - Q2_K,
+ * IQ2_XXS, Q4_K, Q5_K, Q6_K, Q3_K, IQ4_XS, IQ4_NL, NVFP4 (the expert-only
+ * formats return 0, as there); in_dim % 256 == 0. 5 or more tokens on Q4_K,
+ * Q5_K, Q6_K or NVFP4 run the int8 matrix-core GEMM.
  * Replaces pulsar_matmul_kq (pulsar_kernels.cu:4895). */
 int pulsar_matmul_kq(void *out, const void *w, const void *xq, uint32_t in_dim,
                      uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes,
@@ -130,8 +137,10 @@ int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *sta
                                    uint32_t act_op);
 
 /* Grouped down stage: partial[t][s][r] = down_r(group of (t,s)) . midq[t][s]
- * for every listed pair; unlisted (t, s) are left untouched (the caller
- * zeroes partial first). Replaces pulsar_moe_down_grouped (pulsar_kernels.cu:3537). */
+ * for every listed pair; unlisted (t, s) are left untouched, so the caller
+ * zeroes partial before every layer (crates/engine/src/lib.rs:8481-8482):
+ * pulsar_moe_slot_sum reads every slot. Replaces pulsar_moe_down_grouped
+ * (pulsar_kernels.cu:3537). */
 int pulsar_moe_down_grouped(void *partial, const void *gptrs, const void *starts,
                             const void *pairs, const void *midq, uint32_t mid_dim,
                             uint32_t out_dim, uint32_t n_used, uint32_t n_group,
@@ -289,10 +298,10 @@ int pulsar_moe_down_biased(void *out, const void *ptrs, const void *weights, con
                            uint64_t row_bytes, uint32_t quant);
 
 /* Selects the stream every later launch from the calling thread goes to
- * (NULL restores the null stream, the default). No counterpart in the
- * reference, whose launches always use the per-thread default stream
- * (crates/kernels/build.rs:42-48); it lets a caller capture the path into a
- * HIP graph on a capture stream. Returns 1. */
+ * (NULL restores the per-thread default stream, the default). No
+ * counterpart in the reference, whose launches always use the per-thread
+ * default stream (crates/kernels/build.rs:42-48); it lets a caller capture
+ * the path into a graph on a stream of its own. Returns 1. */
 int pulsar_set_stream(void *stream);
 
 /* Streaming-read probe: reads `bytes` (a multiple of 16) from buf through

@@ -73,6 +73,46 @@ __global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
     }
 }
 
+// Rows wider than the register-resident unit layout holds (more than 8
+// units per lane: in_dim > 32768). A wave takes one row and walks it in
+// slices of 16 super-blocks (64 units, one per lane): each slice's weight
+// units and activation slices are loaded, the lane's super-block values are
+// added to its running sum, and the row total is the fixed tree of the
+// lanes' sums. T tokens per launch row (grid.y covers the rest).
+template <uint32_t Q, uint32_t T>
+__global__ __launch_bounds__(256) void matvec_wide_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
+                                                          const pulsar_block_q8_K *__restrict__ xq, uint32_t n_units,
+                                                          uint32_t nblk32, uint32_t in_blocks, uint32_t out_dim,
+                                                          uint32_t n_tok, uint64_t row_bytes) {
+    PK_FMT_LUT(Q)
+    const uint32_t row = blockIdx.x * 4u + threadIdx.x / 64u;
+    if (row >= out_dim) return;  // whole wave
+    const uint32_t t0 = blockIdx.y * T;
+    const uint8_t *wr = w + (uint64_t)row * row_bytes;
+    float acc[T];
+#pragma unroll
+    for (uint32_t t = 0; t < T; t++) acc[t] = 0.0f;
+    for (uint32_t u0 = 0; u0 < n_units; u0 += 64u) {
+        RowGeom rg = row_geom<6>(n_units - u0 < 64u ? n_units - u0 : 64u, nblk32, 6u);
+        const uint32_t sb0 = u0 / 4u;
+        typename Fmt<Q>::W wu[1];
+        load_row_w<Q, 1>(wr + (uint64_t)sb0 * Fmt<Q>::kSbBytes, rg, wu);
+#pragma unroll
+        for (uint32_t t = 0; t < T; t++) {
+            const uint32_t tok = t0 + t < n_tok ? t0 + t : n_tok - 1u;
+            Act a[1];
+            load_row_acts<Q, 1>(xq + (uint64_t)tok * in_blocks + sb0, rg, a);
+            acc[t] += row_partial<Q, 1>(true, rg, wu, a, lut);
+        }
+    }
+    const RowGeom rg = row_geom<6>(64u, nblk32, 6u);
+#pragma unroll
+    for (uint32_t t = 0; t < T; t++) {
+        const float v = row_finish(acc[t], rg);
+        if (rg.holds_row() && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = v;
+    }
+}
+
 #ifndef PK_MV_RPW
 #define PK_MV_RPW 1
 #endif
@@ -130,7 +170,14 @@ static int dispatch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K
     } else if (upl <= 8u) {
         PK_MV(1, 8, 1);
     } else {
-        return reject("matmul_kq (in_dim above 32768)");
+        // wider rows: one wave per row, streamed in 16-super-block slices
+        const dim3 grid((out_dim + 3u) / 4u, n_tok <= 1u ? 1u : (n_tok + 3u) / 4u);
+        if (n_tok == 1u)
+            hipLaunchKernelGGL((matvec_wide_kernel<Q, 1>), grid, dim3(256), 0, pk::stream(), out, w, xq, n_units,
+                               nblk32, in_blocks, out_dim, n_tok, row_bytes);
+        else
+            hipLaunchKernelGGL((matvec_wide_kernel<Q, 4>), grid, dim3(256), 0, pk::stream(), out, w, xq, n_units,
+                               nblk32, in_blocks, out_dim, n_tok, row_bytes);
     }
 #undef PK_MV
     return launch_ok("matmul_kq launch");

@@ -355,3 +355,61 @@ def test_c5_decode_layer_full_shape(dev):
     for j in range(n_slots):
         scale[0] += np.abs(sw_d[0, j] * L.bank.down_b[int(slots[0, j])].astype(np.float64))
     _check(s.name + "/down_biased", down(out), want_b, scale, False)
+
+
+@pytest.mark.parametrize("quant,stage", [(QUANT_Q2_K, "pair"), (QUANT_Q2_K, "down"), (QUANT_Q4_K, "pair"),
+                                         (QUANT_IQ2_XXS, "down"), (QUANT_Q6_K, "down"), (fm.QUANT_MXFP4, "pair")],
+                         ids=lambda v: fm.NAMES.get(v, v) if isinstance(v, int) else v)
+def test_grouped_row_tiles_partial_last_block(dev, quant, stage):
+    """A chunk over 128 experts (16 tokens, top-8) makes the grouped kernel
+    stream several 64-row tiles per block; 1600 rows (25 tiles) leave the
+    last block of each group a partial one. Every (pair, row) against the
+    oracle's row dots: the pair stage's glu * weight, the down stage's
+    per-pair partial rows."""
+    E, n_tok, k, n_rows = 128, 16, 8, 1600
+    k_dim = 1024 if stage == "pair" else 512
+    if quant == fm.QUANT_MXFP4:
+        k_dim = 960
+    rng = np.random.default_rng(n_rows + quant)
+    rb = row_bytes(quant, k_dim)
+    mats = [synth.quant_matrix(quant, E * n_rows, k_dim, synth.rng_for(quant, f"rt{stage}{m}")).reshape(E, n_rows, rb)
+            for m in range(2 if stage == "pair" else 1)]
+    devs = [up(np.concatenate([m.reshape(-1), np.zeros(256, np.uint8)])) for m in mats]
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(n_tok)])
+    w = rng.uniform(0.1, 1.0, (n_tok, k)).astype(np.float32)
+    n_act = n_tok if stage == "pair" else n_tok * k
+    xq = oracle.quantize_q8_k(rng.standard_normal((n_act, k_dim)).astype(np.float32))
+    ids, starts, pairs = synth.csr_by_expert(sel, k)
+    n_group = E  # the device CSR's max_groups: groups past the distinct count are empty
+    entries = []
+    for g in range(n_group):
+        if g < len(ids):
+            e = int(ids[g])
+            a = [d.data_ptr() + e * n_rows * rb for d in devs]
+            entries.append((a[0], a[-1], 0) if stage == "pair" else (0, 0, a[0]))
+        else:
+            entries.append((0, 0, 0))
+    st = np.concatenate([starts, np.full(n_group - len(ids), starts[-1], np.uint32)])
+    gptrs = up(K.expert_ptrs(entries))
+    out = zeros_f32((n_tok * k, n_rows))
+    if stage == "pair":
+        K.moe_pair_swiglu_grouped(out, gptrs, up(st), up(pairs), up_f32(w), up(xq), k_dim, n_rows, k, n_group, rb,
+                                  quant, 0)
+    else:
+        K.moe_down_grouped(out, gptrs, up(st), up(pairs), up(xq), k_dim, n_rows, k, n_group, rb, quant)
+    got = down(out)
+    for t in range(n_tok):
+        for s in range(k):
+            e, so = int(sel[t, s]), t * k + s
+            if stage == "pair":
+                g, ag = oracle.rows_dot(mats[0][e], rb, n_rows, xq[t:t + 1], k_dim, 1, quant, THREADS)
+                u, au = oracle.rows_dot(mats[1][e], rb, n_rows, xq[t:t + 1], k_dim, 1, quant, THREADS)
+                want = np.array([oracle.glu(float(a), float(b), 0) * w[t, s] for a, b in zip(g[0], u[0])])
+                bound = TOL_REL * w[t, s] * (1.5 * (np.abs(u[0]) + 1) * ag[0] + (np.abs(g[0]) + 1) * au[0])
+                bound += 4e-7 * np.abs(want) + 1e-30
+                err = np.abs(got[so].astype(np.float64) - want)
+                assert (err <= bound).all(), (t, s, float(err.max()))
+            else:
+                v, a = oracle.rows_dot(mats[0][e], rb, n_rows, xq[so:so + 1], k_dim, 1, quant, THREADS)
+                err = np.abs(got[so].astype(np.float64) - v[0])
+                assert (err <= TOL_REL * a[0] + 1e-30).all(), (t, s, float(err.max()))

@@ -201,3 +201,38 @@ def test_matvec_rejects_moe_only_formats(dev):
               fm.QUANT_IQ2_S, fm.QUANT_IQ1_S, fm.QUANT_MXFP4):
         with pytest.raises(K.KernelError):
             K.matmul_kq(buf, buf, buf, 256, 4, 1, row_bytes(q, 256), q)
+
+
+@pytest.mark.parametrize("quant", [QUANT_Q4_K, QUANT_Q6_K, QUANT_Q2_K, QUANT_IQ2_XXS, fm.QUANT_IQ4_NL, fm.QUANT_Q3_K],
+                         ids=lambda q: fm.NAMES[q])
+@pytest.mark.parametrize("n,rows,n_tok", [(36864, 9, 1), (40960, 13, 3), (33024, 6, 6)])
+def test_matvec_rows_wider_than_32768(dev, quant, n, rows, n_tok):
+    """Rows of more than 32768 values (the reference accepts any multiple of
+    256, pulsar_kernels.cu:4904): the lane path walks them in 16-super-block
+    slices (n_tok >= 5 on Q4_K / Q6_K goes to the MFMA GEMM). Seeded
+    weights within 1e-5 * sum_b |f_b|, and unit scales bit-exact."""
+    w = synth.quant_matrix(quant, rows, n, synth.rng_for(n + rows, "wide"))
+    x = rng.standard_normal((n_tok, n)).astype(np.float32)
+    xq = oracle.quantize_q8_k(x)
+    rb = row_bytes(quant, n)
+    out = zeros_f32((n_tok, rows))
+    K.matmul_kq(out, up(w), up(xq), n, rows, n_tok, rb, quant)
+    got = down(out)
+    for t in range(n_tok):
+        vals, scale = zip(*(oracle.vec_dot(quant, w[r], xq[t], n) for r in range(rows)))
+        assert_rows_close(got[t], np.array(vals, np.float32), np.array(scale), f"q{quant} n{n} t{t}")
+    if quant in (QUANT_Q4_K, QUANT_Q6_K, QUANT_Q2_K, QUANT_IQ2_XXS, fm.QUANT_Q3_K):
+        wu = unit_scale_matrix(quant, rows, n, n)
+        nb = n // 256  # q8_K rows with d = 1 and quants in [-12, 12]: sums stay exact in fp32
+        qs = rng.integers(-12, 13, (n_tok, nb, 256)).astype(np.int8)
+        blk = np.zeros((n_tok, nb, 292), np.uint8)
+        blk[..., 0:4] = np.array([1.0], np.float32).view(np.uint8)
+        blk[..., 4:260] = qs.view(np.uint8)
+        blk[..., 260:292] = qs.reshape(n_tok, nb, 16, 16).astype(np.int16).sum(-1).astype(np.int16).view(
+            np.uint8).reshape(n_tok, nb, 32)
+        xu = blk.reshape(n_tok, nb * 292)
+        out.zero_()
+        K.matmul_kq(out, up(wu), up(xu), n, rows, n_tok, rb, quant)
+        want = oracle.matmul_kq(wu, xu, n, rows, n_tok, rb, quant)
+        assert np.abs(want).max() < 2**24
+        assert np.array_equal(down(out), want)
