@@ -23,19 +23,19 @@ constexpr uint32_t kFusedMaxSlots = 64;    // k_used + n_shared
 constexpr uint32_t kFusedMaxActLds = 65536; // staged mid rows of one token
 
 
-// Blocks [0, gemv_blocks) compute logits (one wave per (row, TG tokens)),
+// Blocks [0, gemv_blocks) compute logits (one block per (row, TG tokens),
+// the same reduction as pulsar_matmul_f32 so the logits are bit-identical),
 // the rest quantize x (one wave per 256-value block).
 template <uint32_t TG>
 __global__ __launch_bounds__(256) void router_logits_q8_kernel(
         float *__restrict__ logits, pulsar_block_q8_K *__restrict__ xq, const float *__restrict__ x,
         const float *__restrict__ w, const float *__restrict__ bias, uint32_t in_dim, uint32_t n_expert,
-        uint32_t n_tok, uint32_t n_work, uint32_t gemv_blocks, uint32_t nb) {
-    const uint32_t wave = threadIdx.x >> 6;
+        uint32_t n_tok, uint32_t gemv_blocks, uint32_t nb) {
     if (blockIdx.x < gemv_blocks) {
-        gemv_wave<TG>(logits, w, x, bias, in_dim, n_expert, n_tok, blockIdx.x * 4u + wave, n_work);
+        gemv_block<TG>(logits, w, x, bias, in_dim, n_expert, n_tok, blockIdx.x);
         return;
     }
-    const uint32_t gblk = (blockIdx.x - gemv_blocks) * 4u + wave;
+    const uint32_t gblk = (blockIdx.x - gemv_blocks) * 4u + (threadIdx.x >> 6);
     if (gblk >= n_tok * nb) return;  // whole wave
     const uint32_t row = gblk / nb, b = gblk - row * nb;
     quantize_block_wave<4u, 260u>(x + (uint64_t)row * in_dim, in_dim, b, (uint8_t *)(xq + gblk));
@@ -342,17 +342,17 @@ extern "C" int pulsar_router_logits_q8(void *logits, void *xq, const void *x, co
     const uint64_t work = (uint64_t)n_expert * ((n_tok + tg - 1u) / tg);
     const uint32_t nb = (in_dim + 255u) / 256u;
     const uint64_t qblocks = ((uint64_t)n_tok * nb + 3u) / 4u;
-    const uint64_t gemv_blocks = (work + 3u) / 4u;
+    const uint64_t gemv_blocks = work;
     if (gemv_blocks + qblocks > 0x7fffffffull) return reject("router logits q8 (size)");
     const dim3 grid((uint32_t)(gemv_blocks + qblocks));
     if (tg == 1u)
         hipLaunchKernelGGL(router_logits_q8_kernel<1>, grid, dim3(256), 0, pk::stream(), (float *)logits,
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
-                           in_dim, n_expert, n_tok, (uint32_t)work, (uint32_t)gemv_blocks, nb);
+                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb);
     else
         hipLaunchKernelGGL(router_logits_q8_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)logits,
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
-                           in_dim, n_expert, n_tok, (uint32_t)work, (uint32_t)gemv_blocks, nb);
+                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb);
     return launch_ok("router logits q8 launch");
 }
 

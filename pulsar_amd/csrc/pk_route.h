@@ -157,19 +157,22 @@ PK_DEV void route_lane(const float *lg, const float *rbias, uint32_t n_expert, u
     e = win[0];
 }
 
-// f32 GEMV for router logits: one wave per (row, group of TG tokens);
-// lanes stride over K with 16-byte loads of the row and of the TG token
-// vectors, then a wave reduction per token; bias (if any) is added to the
-// finished sum, as a separate bias pass would. Waves of a block take
-// consecutive rows of the same token group, so the token vectors are shared
-// through the cache.
+// f32 GEMV for router logits, one block of 256 threads per (row, group of
+// TG tokens): the row's K is split over the block's threads (thread i takes
+// float4 pieces i, i + 256, ... so every wave-wide load is one contiguous
+// KiB), all of a batch's loads (4 pieces of the row and of each token)
+// issued before any is used. Each thread sums its products in order, the
+// wave sums its lanes by a fixed butterfly, and the block adds its 4 waves'
+// sums in wave order; the bias (if any) is added to the finished sum, as a
+// separate bias pass would. A router row is one memory round trip.
 template <uint32_t TG>
-PK_DEV void gemv_wave(float *__restrict__ out, const float *__restrict__ w, const float *__restrict__ x,
-                      const float *__restrict__ bias, uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
-                      uint32_t gw, uint32_t n_work) {
-    const uint32_t lane = threadIdx.x & 63u;
-    if (gw >= n_work) return;  // wave-uniform
-    const uint32_t row = gw % out_dim, t0 = (gw / out_dim) * TG;
+PK_DEV void gemv_block(float *__restrict__ out, const float *__restrict__ w, const float *__restrict__ x,
+                       const float *__restrict__ bias, uint32_t in_dim, uint32_t out_dim, uint32_t n_tok,
+                       uint32_t item) {
+    constexpr uint32_t B = 4;  // float4 pieces per thread per batch
+    __shared__ float part[4][TG];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t row = item % out_dim, t0 = (item / out_dim) * TG;
     const float *wr = w + (uint64_t)row * in_dim;
     const float *xr[TG];
 #pragma unroll
@@ -178,27 +181,46 @@ PK_DEV void gemv_wave(float *__restrict__ out, const float *__restrict__ w, cons
 #pragma unroll
     for (uint32_t t = 0; t < TG; t++) acc[t] = 0.0f;
     const uint32_t n4 = in_dim / 4u;
-    for (uint32_t i = lane; i < n4; i += 64u) {
-        const uint4 a = ld128((const uint8_t *)(wr + 4u * i));
+    for (uint32_t base = 0; base < n4; base += 256u * B) {
+        uint4 wv[B], xv[TG][B];
 #pragma unroll
-        for (uint32_t t = 0; t < TG; t++) {
-            const uint4 b = ld128((const uint8_t *)(xr[t] + 4u * i));
-            acc[t] += __uint_as_float(a.x) * __uint_as_float(b.x);
-            acc[t] += __uint_as_float(a.y) * __uint_as_float(b.y);
-            acc[t] += __uint_as_float(a.z) * __uint_as_float(b.z);
-            acc[t] += __uint_as_float(a.w) * __uint_as_float(b.w);
+        for (uint32_t b = 0; b < B; b++) {
+            const uint32_t i = base + tid + 256u * b, ic = i < n4 ? i : n4 - 1u;  // clamped: no branch
+            wv[b] = ld128((const uint8_t *)(wr + 4u * ic));
+#pragma unroll
+            for (uint32_t t = 0; t < TG; t++) xv[t][b] = ld128((const uint8_t *)(xr[t] + 4u * ic));
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < B; b++) {
+            if (base + tid + 256u * b >= n4) break;
+            const uint4 a = wv[b];
+#pragma unroll
+            for (uint32_t t = 0; t < TG; t++) {
+                const uint4 c = xv[t][b];
+                acc[t] += __uint_as_float(a.x) * __uint_as_float(c.x);
+                acc[t] += __uint_as_float(a.y) * __uint_as_float(c.y);
+                acc[t] += __uint_as_float(a.z) * __uint_as_float(c.z);
+                acc[t] += __uint_as_float(a.w) * __uint_as_float(c.w);
+            }
         }
     }
-    for (uint32_t i = 4u * n4 + lane; i < in_dim; i += 64u) {
+    for (uint32_t i = 4u * n4 + tid; i < in_dim; i += 256u) {
 #pragma unroll
         for (uint32_t t = 0; t < TG; t++) acc[t] += wr[i] * xr[t][i];
     }
-    const float b = bias ? bias[row] : 0.0f;
 #pragma unroll
     for (uint32_t t = 0; t < TG; t++) {
-        float v = group_sum<64>(acc[t]);
-        if (bias) v += b;
-        if (lane == 0 && t0 + t < n_tok) out[(uint64_t)(t0 + t) * out_dim + row] = v;
+        const float v = group_sum<64>(acc[t]);
+        if (lane == 0) part[wave][t] = v;
+    }
+    __syncthreads();
+    if (tid < TG && t0 + tid < n_tok) {
+        float v = part[0][tid];
+        v += part[1][tid];
+        v += part[2][tid];
+        v += part[3][tid];
+        if (bias) v += bias[row];
+        out[(uint64_t)(t0 + tid) * out_dim + row] = v;
     }
 }
 

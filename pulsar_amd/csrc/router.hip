@@ -11,8 +11,8 @@ namespace pk {
 template <uint32_t TG>
 __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out, const float *__restrict__ w,
                                                          const float *__restrict__ x, uint32_t in_dim,
-                                                         uint32_t out_dim, uint32_t n_tok, uint32_t n_work) {
-    gemv_wave<TG>(out, w, x, nullptr, in_dim, out_dim, n_tok, blockIdx.x * 4u + (threadIdx.x >> 6), n_work);
+                                                         uint32_t out_dim, uint32_t n_tok) {
+    gemv_block<TG>(out, w, x, nullptr, in_dim, out_dim, n_tok, blockIdx.x);
 }
 
 // x[r][i] += bias[i] (pulsar_kernels.cu:3621-3629)
@@ -105,17 +105,17 @@ __global__ __launch_bounds__(64) void router_select_kernel(int32_t *__restrict__
 extern "C" int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32_t in_dim,
                                  uint32_t out_dim, uint32_t n_tok) {
     if (!out || !w || !x || in_dim == 0 || out_dim == 0 || n_tok == 0) return pk::reject("matmul f32");
-    // tokens in groups of 4 (1 for a single token); one wave per (row, group)
+    // tokens in groups of 4 (1 for a single token); one block per (row, group)
     const uint32_t tg = n_tok == 1u ? 1u : 4u;
     const uint64_t work = (uint64_t)out_dim * ((n_tok + tg - 1u) / tg);
-    if (work > 0xffffffffull - 3u) return pk::reject("matmul f32 (size)");
-    const dim3 grid((uint32_t)((work + 3u) / 4u));
+    if (work > 0x7fffffffull) return pk::reject("matmul f32 (size)");
+    const dim3 grid((uint32_t)work);
     if (tg == 1u)
         hipLaunchKernelGGL(pk::matmul_f32_kernel<1>, grid, dim3(256), 0, pk::stream(), (float *)out,
-                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, (uint32_t)work);
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
     else
         hipLaunchKernelGGL(pk::matmul_f32_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)out,
-                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, (uint32_t)work);
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
     return pk::launch_ok("matmul f32 launch");
 }
 
