@@ -41,37 +41,6 @@ __global__ __launch_bounds__(256) void router_logits_q8_kernel(
     quantize_block_wave<4u, 260u>(x + (uint64_t)row * in_dim, in_dim, b, (uint8_t *)(xq + gblk));
 }
 
-// Routing of one token for slot `slot`, computed by the calling wave (every
-// wave of the block computes the same): the expert pointers and router
-// weight of the slot, with the weight normalisation of router_select_kernel
-// (mode 1: softmax over the winners with a sequential exp-sum; mode 0:
-// probabilities over their sequential sum, floored at 2^-14).
-struct SlotRoute {
-    pulsar_expert_ptrs p;
-    float w;
-    int32_t e;
-};
-
-template <uint32_t J>
-PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used,
-                            float scale, uint32_t mode, const pulsar_expert_bank &bank, const SharedSlots &shared,
-                            uint32_t slot) {
-    int32_t e;
-    float wk;
-    route_lane<J>(lg, rbias, n_expert, k_used, scale, mode, e, wk);
-    SlotRoute r;
-    if (slot < k_used) {
-        r.e = __builtin_amdgcn_readlane(e, (int)slot);
-        r.w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), (int)slot));
-        r.p = bank_ptrs(bank, n_expert, r.e);
-    } else {
-        r.e = -1;
-        r.w = 1.0f;
-        r.p = shared.p[slot - k_used];
-    }
-    return r;
-}
-
 // grid (row blocks, k_used + n_shared, n_tok); the pair stage of
 // moe_pair_kernel for the slot's expert, routed in-block.
 template <uint32_t Q, uint32_t UPLMAX, uint32_t J, uint32_t NPL, uint32_t RPW>
@@ -233,20 +202,6 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
 }
 
 // ------------------------------------------------------------ dispatch --
-
-struct FGeo {
-    uint32_t n_units, nblk32, l2, upl, blocks;
-};
-
-static FGeo fgeo_for(uint32_t quant, uint32_t k_dim) {
-    FGeo g;
-    g.n_units = units_per_row(quant, k_dim);
-    g.nblk32 = (k_dim + 31u) / 32u;
-    g.l2 = lpr_log2_for(g.n_units);
-    g.upl = (g.n_units + (1u << g.l2) - 1u) >> g.l2;
-    g.blocks = (k_dim + 255u) / 256u;
-    return g;
-}
 
 // F::template run<Q, UPLMAX>() for the run-time (quant, upl), up to 4
 // units per lane.

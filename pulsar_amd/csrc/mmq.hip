@@ -505,15 +505,21 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
 // one MFMA per group gives sumi, bsum += sumi (2 (aux1 >> 28) + 1), super-
 // block value 0.125 xd yd bsum (cpu_dot.rs:92-122).
 // Per (row, pair) the super-block values are added in order; the row's
-// value is then complete (no cross-wave sum).
+// value is then complete (no cross-wave sum). Formats with a min term (Q2_K,
+// Q4_K, Q5_K) form each super-block value in the CPU lane's operation order,
+// since its two products can cancel; the single-product formats (Q6_K,
+// IQ2_XXS, MXFP4) fold the value into the sum with one fused multiply-add,
+// within an ulp of the lane's value.
 template <uint32_t Q>
 struct GmmqFmt;
 // Row super-block copies: kPieces 16-byte pieces (piece_off) to slot 16c,
 // kTails small loads (tail_off, kTailBytes each) to kTailSlot + c. `lim`
-// bounds the clamped unit (super-blocks, or 32-blocks for MXFP4).
+// bounds the clamped unit (super-blocks, or 32-blocks for MXFP4; kLimPerSb
+// of them per super-block); consecutive super-blocks are kSbBytes apart.
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q2_K> {
     static constexpr uint32_t kPieces = 5, kTails = 1, kTailBytes = 4;
+    static constexpr uint32_t kSbBytes = 84, kLimPerSb = 1;
     static constexpr uint32_t kTailSlot = 80;  // d, dmin
     static constexpr uint32_t kSlot = 96;      // LDS bytes per row super-block
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -524,6 +530,7 @@ struct GmmqFmt<PULSAR_QUANT_Q2_K> {
 template <>
 struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
     static constexpr uint32_t kPieces = 4, kTails = 1, kTailBytes = 4;
+    static constexpr uint32_t kSbBytes = 66, kLimPerSb = 1;
     static constexpr uint32_t kTailSlot = 64;  // d (the upper 2 bytes unused)
     static constexpr uint32_t kSlot = 80;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -536,6 +543,7 @@ struct GmmqFmt<PULSAR_QUANT_MXFP4> {
     // super-block = 8 blocks of 17 bytes; block c's qs to slot 16c, its e
     // to slot 128 + c
     static constexpr uint32_t kPieces = 8, kTails = 8, kTailBytes = 1;
+    static constexpr uint32_t kSbBytes = 136, kLimPerSb = 8;  // lim counts 32-blocks
     static constexpr uint32_t kTailSlot = 128;
     static constexpr uint32_t kSlot = 144;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -550,6 +558,7 @@ struct GmmqFmt<PULSAR_QUANT_MXFP4> {
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q4_K> {
     static constexpr uint32_t kPieces = 9, kTails = 0, kTailBytes = 4;  // the whole 144 bytes
+    static constexpr uint32_t kSbBytes = 144, kLimPerSb = 1;
     static constexpr uint32_t kTailSlot = 0;
     static constexpr uint32_t kSlot = 144;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -560,6 +569,7 @@ struct GmmqFmt<PULSAR_QUANT_Q4_K> {
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q5_K> {
     static constexpr uint32_t kPieces = 11, kTails = 0, kTailBytes = 4;  // the whole 176 bytes
+    static constexpr uint32_t kSbBytes = 176, kLimPerSb = 1;
     static constexpr uint32_t kTailSlot = 0;
     static constexpr uint32_t kSlot = 176;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -570,6 +580,7 @@ struct GmmqFmt<PULSAR_QUANT_Q5_K> {
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q6_K> {
     static constexpr uint32_t kPieces = 13, kTails = 1, kTailBytes = 2;  // bytes 0..207, then d
+    static constexpr uint32_t kSbBytes = 210, kLimPerSb = 1;
     static constexpr uint32_t kTailSlot = 208;
     static constexpr uint32_t kSlot = 224;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
@@ -608,6 +619,24 @@ PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
         y &= 0x007f007fu;
     }
     return __builtin_amdgcn_perm(y, x, 0x06040200u);  // bytes 0, 2 of x, then of y
+}
+
+// Tiles of at most 4 pairs: the MFMA result of pairs 0..3 sits in the kq = 0
+// lanes (lane i, element r = pair r); this moves element p of lane i to lane
+// i + 16 p, so every lane holds one (row, pair) value and the fp32 epilogue
+// runs once per lane instead of once per element (two permlane16 swaps,
+// one permlane32 swap).
+PK_DEV uint32_t gather_pairs(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3) {
+    const auto a = __builtin_amdgcn_permlane16_swap(d0, d1, false, false);  // rows: d0.0 d1.0 ..
+    const auto c = __builtin_amdgcn_permlane16_swap(d2, d3, false, false);  // rows: d2.0 d3.0 ..
+    return __builtin_amdgcn_permlane32_swap(a[0], c[0], false, false)[0];    // d0.0 d1.0 d2.0 d3.0
+}
+PK_DEV int32_t gather_pairs(const v4i &d) {
+    return (int32_t)gather_pairs((uint32_t)d[0], (uint32_t)d[1], (uint32_t)d[2], (uint32_t)d[3]);
+}
+PK_DEV float gather_pairs(const float (&f)[4]) {
+    return __uint_as_float(gather_pairs(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                                        __float_as_uint(f[3])));
 }
 
 // Waves per block, 16 rows each. MXFP4 blocks take 8: their pair tiles are
@@ -668,26 +697,31 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     // kPieces): consecutive lanes on consecutive bytes of a row's S super-
     // blocks. Lanes past the last piece load one too (never stored), so
     // every lane issues the same loads and the waits count them exactly.
+    // wsrc: the piece's address in step 0 (super-block sl of its row,
+    // clamped to the row's last unit), wlim: the offset from there to the
+    // piece in the row's last unit
     const uint8_t *wsrc[kWj];
-    uint32_t wsc[kWj], wdst[kWj];  // wsc = slot << 8 | piece
+    uint32_t wlim[kWj], wdst[kWj];
 #pragma unroll
     for (uint32_t j = 0; j < kWj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kWp ? q : kWp - 1u;
         const uint32_t c = qq % F::kPieces, rs = qq / F::kPieces, sl = rs % S, rm = rs / S;
-        wsrc[j] = row_src(rm / 16u, rm % 16u);
-        wsc[j] = sl << 8 | c;
+        const uint32_t o0 = F::piece_off(sl, c, lim);
+        wsrc[j] = row_src(rm / 16u, rm % 16u) + o0;
+        wlim[j] = F::piece_off(lim, c, lim) - o0;
         wdst[j] = q < kWp ? (rm * kRowL + sl * F::kSlot + 16u * c) : UINT32_MAX;
     }
     // tails (d / dmin, MXFP4 e): kTails per (matrix, row, super-block of the step)
     const uint8_t *tsrc[kTjA];
-    uint32_t tsc[kTjA], tdst[kTjA];
+    uint32_t tlim[kTjA], tdst[kTjA];
 #pragma unroll
     for (uint32_t j = 0; j < kTj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
         const uint32_t c = qq % (F::kTails ? F::kTails : 1u), rs = qq / (F::kTails ? F::kTails : 1u);
         const uint32_t sl = rs % S, rm = rs / S;
-        tsrc[j] = row_src(rm / 16u, rm % 16u);
-        tsc[j] = sl << 8 | c;
+        const uint32_t o0 = F::tail_off(sl, c, lim);
+        tsrc[j] = row_src(rm / 16u, rm % 16u) + o0;
+        tlim[j] = F::tail_off(lim, c, lim) - o0;
         tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot + c) : UINT32_MAX;
     }
     uint8_t *wl_w = &wl[wave][0];
@@ -706,33 +740,47 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         uint4 wv[kWj];
         uint32_t tv[kTjA];
         auto issue = [&](uint32_t step) {
+            // the step-0 address plus the step's uniform offset, held at the
+            // lane's last unit of the row (units past the row are loaded
+            // from it, never used): one min and one 64-bit add per load
+            const uint32_t so = step * S * F::kSbBytes;
 #pragma unroll
-            for (uint32_t j = 0; j < kWj; j++)
-                wv[j] = ldw128(wsrc[j] + F::piece_off(step * S + (wsc[j] >> 8), wsc[j] & 0xffu, lim));
+            for (uint32_t j = 0; j < kWj; j++) wv[j] = ldw128(wsrc[j] + (so < wlim[j] ? so : wlim[j]));
 #pragma unroll
             for (uint32_t j = 0; j < kTj; j++) {
-                const uint8_t *tp = tsrc[j] + F::tail_off(step * S + (tsc[j] >> 8), tsc[j] & 0xffu, lim);
+                const uint8_t *tp = tsrc[j] + (so < tlim[j] ? so : tlim[j]);
                 tv[j] = F::kTailBytes == 4u ? ldw32(tp) : F::kTailBytes == 2u ? (uint32_t)ldw16(tp) : ldw8(tp);
             }
         };
         // lane (pair i, kq): its pair's record (the last pair's past the tile)
         const uint8_t *ar = acts_lds + (i < m ? i : m - 1u) * act_bytes;
-        float acc[NM][4];
+        // tiles of at most 4 pairs (wave-uniform): lane (row i, pair kq)
+        // accumulates acs; larger tiles: lane (row i, kq) pairs 4 kq + r in
+        // acc. Q4_K, Q5_K and Q6_K keep the one path: the second one costs
+        // their pair stages occupancy (Q4_K 127 -> 169 VGPRs)
+        constexpr bool kSmallPath = Q == PULSAR_QUANT_Q2_K || kIq2 || kMx;
+        const bool small = kSmallPath && m <= 4u;
+        float acc[NM][4], acs[NM];
 #pragma unroll
-        for (uint32_t mt = 0; mt < NM; mt++)
+        for (uint32_t mt = 0; mt < NM; mt++) {
+            acs[mt] = 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
+        }
         // super-block sb from the wave's LDS slot ws (row i of matrix 0)
         auto sb_compute = [&](uint32_t sb, const uint8_t *ws) {
             const uint8_t *rec = ar + sb * kActLdsPitch;  // d @0, q8 values @16, bsums @272
             // pairs past the tile read the last pair's values: their MFMA
             // rows and sums are never stored
             float yd[4];
+            if (!small) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t pi = 4u * kq + r < m ? 4u * kq + r : m - 1u;
-                yd[r] = *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch);
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t pi = 4u * kq + r < m ? 4u * kq + r : m - 1u;
+                    yd[r] = *(const float *)(acts_lds + pi * act_bytes + sb * kActLdsPitch);
+                }
             }
+            const float yd1 = *(const float *)(acts_lds + (kq < m ? kq : m - 1u) * act_bytes + sb * kActLdsPitch);
             auto a_at = [&](uint32_t t) { return *(const uint2 *)(rec + 16u + 32u * t + 8u * kq); };
             if constexpr (kMx) {
                 // lane group kq: values {0, 16, 8, 24}[kq] + [0, 8) of a block,
@@ -764,9 +812,14 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                     }
                 }
 #pragma unroll
-                for (uint32_t mt = 0; mt < NM; mt++)
+                for (uint32_t mt = 0; mt < NM; mt++) {
+                    if (small) {
+                        acs[mt] = __builtin_fmaf(yd1, gather_pairs(f[mt]), acs[mt]);
+                    } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[mt][r] += yd[r] * f[mt][r];
+                        for (int r = 0; r < 4; r++) acc[mt][r] = __builtin_fmaf(yd[r], f[mt][r], acc[mt][r]);
+                    }
+                }
             } else if constexpr (Q == PULSAR_QUANT_Q6_K) {
                 // two MFMAs per 32-value step (both 16-value scale groups, then
                 // the first alone): sc0 D0 + sc1 D1 = (sc0 - sc1) D_lo + sc1 D_all
@@ -796,8 +849,13 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
                     const float xd = f16f((uint16_t)wv[mt].d);
+                    if (small) {
+                        const v4i is = {isum[mt][0], isum[mt][1], isum[mt][2], isum[mt][3]};
+                        acs[mt] = __builtin_fmaf(xd * yd1, (float)gather_pairs(is), acs[mt]);
+                    } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[mt][r] += xd * yd[r] * (float)isum[mt][r];
+                        for (int r = 0; r < 4; r++) acc[mt][r] = __builtin_fmaf(xd * yd[r], (float)isum[mt][r], acc[mt][r]);
+                    }
                 }
             } else if constexpr (Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q5_K) {
                 // one MFMA per 32-value sub-block, its 6-bit scale on D; the
@@ -834,10 +892,16 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                     const v4i dl = mfma16x16x32(alh, kq < 2u ? make_uint2(mw, 0u) : make_uint2(0u, 0u));
                     const v4i dh = mfma16x16x32(alh, kq < 2u ? make_uint2(0u, 0u) : make_uint2(mw, 0u));
                     const float xd = f16f((uint16_t)wv[mt].hdr.x), xmin = f16f((uint16_t)(wv[mt].hdr.x >> 16));
+                    if (small) {
+                        const v4i is = {isum[mt][0], isum[mt][1], isum[mt][2], isum[mt][3]};
+                        const v4i ms = {dl[0] + 128 * dh[0], dl[1] + 128 * dh[1], dl[2] + 128 * dh[2], dl[3] + 128 * dh[3]};
+                        acs[mt] += xd * yd1 * (float)gather_pairs(is) - xmin * yd1 * (float)gather_pairs(ms);
+                    } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int32_t msum = dl[r] + 128 * dh[r];
-                        acc[mt][r] += xd * yd[r] * (float)isum[mt][r] - xmin * yd[r] * (float)msum;
+                        for (int r = 0; r < 4; r++) {
+                            const int32_t msum = dl[r] + 128 * dh[r];
+                            acc[mt][r] += xd * yd[r] * (float)isum[mt][r] - xmin * yd[r] * (float)msum;
+                        }
                     }
                 }
             } else if constexpr (!kIq2) {
@@ -891,10 +955,15 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                     const v4i dh = mfma16x16x32(alh, kq < 2u ? zero : mn);
                     const uint32_t dd = *(const uint32_t *)(ws + mt * 16u * kRowL + F::kTailSlot);
                     const float xd = f16f((uint16_t)dd), xmin = f16f((uint16_t)(dd >> 16));
+                    if (small) {
+                        const v4i sm = {dl[0] + 128 * dh[0], dl[1] + 128 * dh[1], dl[2] + 128 * dh[2], dl[3] + 128 * dh[3]};
+                        acs[mt] += yd1 * xd * (float)gather_pairs(isum[mt]) - yd1 * xmin * (float)gather_pairs(sm);
+                    } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int32_t summs = dl[r] + 128 * dh[r];
-                        acc[mt][r] += yd[r] * xd * (float)isum[mt][r] - yd[r] * xmin * (float)summs;
+                        for (int r = 0; r < 4; r++) {
+                            const int32_t summs = dl[r] + 128 * dh[r];
+                            acc[mt][r] += yd[r] * xd * (float)isum[mt][r] - yd[r] * xmin * (float)summs;
+                        }
                     }
                 }
             } else {
@@ -924,9 +993,14 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 }
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    const float xd = f16f(*(const uint16_t *)(ws + mt * 16u * kRowL + F::kTailSlot));
+                    const float xd8 = 0.125f * f16f(*(const uint16_t *)(ws + mt * 16u * kRowL + F::kTailSlot));
+                    if (small) {
+                        const v4i bs = {bsum[mt][0], bsum[mt][1], bsum[mt][2], bsum[mt][3]};
+                        acs[mt] = __builtin_fmaf(xd8 * yd1, (float)gather_pairs(bs), acs[mt]);
+                    } else {
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[mt][r] += 0.125f * xd * yd[r] * (float)bsum[mt][r];
+                        for (int r = 0; r < 4; r++) acc[mt][r] = __builtin_fmaf(xd8 * yd[r], (float)bsum[mt][r], acc[mt][r]);
+                    }
                 }
             }
         };
@@ -956,22 +1030,22 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             // this step's LDS reads are consumed before the next copy
             __builtin_amdgcn_wave_barrier();
         }
-        // lane (row i, kq): pairs 4kq + r of the tile
+        // lane (row i, kq): pairs 4kq + r of the tile (small tiles: pair kq)
         const uint32_t orow = rw0 + i;
         if (orow < n_rows) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint32_t pi = 4u * kq + r;
-                if (pi >= m) break;
+                const uint32_t pi = small ? kq : 4u * kq + r;
+                if (pi >= m || (small && r > 0)) break;
                 const uint32_t pr = pr_l[pi];
                 const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
                 if (PAIR) {
-                    float g = acc[0][r], u = acc[NM - 1][r];
+                    float g = small ? acs[0] : acc[0][r], u = small ? acs[NM - 1] : acc[NM - 1][r];
                     if (p.gate_b) g += ldwf(p.gate_b + orow);
                     if (p.up_b) u += ldwf(p.up_b + orow);
                     out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
                 } else {
-                    out[so * n_rows + orow] = acc[0][r];
+                    out[so * n_rows + orow] = small ? acs[0] : acc[0][r];
                 }
             }
         }

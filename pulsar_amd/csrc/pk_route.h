@@ -245,4 +245,36 @@ PK_DEV pulsar_expert_ptrs bank_ptrs(const pulsar_expert_bank &bank, uint32_t n_e
     return p;
 }
 
+// Routing of one token for slot `slot`, computed by the calling wave (every
+// wave of the block computes the same): the expert pointers and router
+// weight of the slot, with the weight normalisation of router_select_kernel
+// (mode 1: softmax over the winners with a sequential exp-sum; mode 0:
+// probabilities over their sequential sum, floored at 2^-14).
+struct SlotRoute {
+    pulsar_expert_ptrs p;
+    float w;
+    int32_t e;
+};
+
+template <uint32_t J>
+PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used,
+                            float scale, uint32_t mode, const pulsar_expert_bank &bank, const SharedSlots &shared,
+                            uint32_t slot) {
+    int32_t e;
+    float wk;
+    route_lane<J>(lg, rbias, n_expert, k_used, scale, mode, e, wk);
+    SlotRoute r;
+    if (slot < k_used) {
+        r.e = __builtin_amdgcn_readlane(e, (int)slot);
+        r.w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), (int)slot));
+        r.p = bank_ptrs(bank, n_expert, r.e);
+    } else {
+        r.e = -1;
+        r.w = 1.0f;
+        r.p = shared.p[slot - k_used];
+    }
+    return r;
+}
+
+
 }  // namespace pk

@@ -36,6 +36,21 @@ static inline uint32_t units_per_row(uint32_t quant, uint32_t in_dim) {
     return 4u * ((in_dim + 255u) / 256u);
 }
 
+// Row geometry of a matrix stage: units per row, 32-value blocks, lanes
+// per row (log2), units per lane and q8_K blocks per activation row.
+struct FGeo {
+    uint32_t n_units, nblk32, l2, upl, blocks;
+};
+static FGeo fgeo_for(uint32_t quant, uint32_t k_dim) {
+    FGeo g;
+    g.n_units = units_per_row(quant, k_dim);
+    g.nblk32 = (k_dim + 31u) / 32u;
+    g.l2 = lpr_log2_for(g.n_units);
+    g.upl = (g.n_units + (1u << g.l2) - 1u) >> g.l2;
+    g.blocks = (k_dim + 255u) / 256u;
+    return g;
+}
+
 // L2 > 0 fixes lanes-per-row at compile time (1 << L2); with L2 == 6 a
 // wave holds one row, so row addresses stay wave-uniform (scalar).
 template <uint32_t L2 = 0>
