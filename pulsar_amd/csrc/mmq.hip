@@ -611,14 +611,12 @@ PK_DEV uint32_t pk_mul16(uint32_t a, uint32_t b) {
 // Two packed int16 -> two bytes (low bytes), for the bsums split
 typedef short pk_short2 __attribute__((ext_vector_type(2)));
 PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
-    if (high) {  // h = b >> 7 (arithmetic), |h| <= 16
-        x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, x) >> (short)7);
-        y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, y) >> (short)7);
-    } else {  // l = b & 127
-        x &= 0x007f007fu;
-        y &= 0x007f007fu;
-    }
-    return __builtin_amdgcn_perm(y, x, 0x06040200u);  // bytes 0, 2 of x, then of y
+    // both splits formed and one kept per lane (selects: a divergent branch
+    // here would split the hot loop into many blocks)
+    const uint32_t hx = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, x) >> (short)7);  // h = b >> 7
+    const uint32_t hy = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, y) >> (short)7);  // |h| <= 16
+    const uint32_t lx = x & 0x007f007fu, ly = y & 0x007f007fu;                                      // l = b & 127
+    return __builtin_amdgcn_perm(high ? hy : ly, high ? hx : lx, 0x06040200u);  // bytes 0, 2 of x, then of y
 }
 
 // Tiles of at most 4 pairs: the MFMA result of pairs 0..3 sits in the kq = 0

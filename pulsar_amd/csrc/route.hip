@@ -74,27 +74,41 @@ PK_DEV uint32_t ptr_hash(uint64_t k) { return (uint32_t)(((k >> 4) * 0x9E3779B97
 // insert, atomic min of the pair index), group ids and group starts by
 // block scans, members scattered to their group's segment and put in pair
 // order by counting the smaller pair indices in the segment.
+// The CSR build's LDS tables (declared by the kernel, cleared by
+// csr_clear before a block barrier that precedes csr_build).
+struct CsrLds {
+    unsigned long long tkey[kHashSlots];
+    uint32_t tfirst[kHashSlots];
+    uint32_t gid_of[kMaxCsrPairs];  // group id, at the index of the group's first pair
+    uint32_t gstart[kMaxCsrPairs + 1];
+    uint32_t fill[kMaxCsrPairs];
+    uint32_t seg[kMaxCsrPairs];  // pair indices by group, unordered within a group
+    uint32_t wsum[kCsrThreads / 64u];
+};
+
+PK_DEV void csr_clear(CsrLds &T) {
+    for (uint32_t h = threadIdx.x; h < kHashSlots; h += kCsrThreads) {
+        T.tkey[h] = 0ull;
+        T.tfirst[h] = UINT32_MAX;
+    }
+    for (uint32_t g = threadIdx.x; g < kMaxCsrPairs; g += kCsrThreads) {
+        T.gstart[g] = 0u;
+        T.fill[g] = 0u;
+    }
+}
+
 template <typename KeyFn, typename PtrFn>
-PK_DEV void csr_build(pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
+PK_DEV void csr_build(CsrLds &T, pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
                       uint32_t *__restrict__ pairs, KeyFn key_of, PtrFn ptrs_of, uint32_t n, uint32_t n_used,
                       uint32_t max_groups) {
-    __shared__ unsigned long long tkey[kHashSlots];
-    __shared__ uint32_t tfirst[kHashSlots];
-    __shared__ uint32_t gid_of[kMaxCsrPairs];  // group id, at the index of the group's first pair
-    __shared__ uint32_t gstart[kMaxCsrPairs + 1];
-    __shared__ uint32_t fill[kMaxCsrPairs];
-    __shared__ uint32_t seg[kMaxCsrPairs];  // pair indices by group, unordered within a group
-    __shared__ uint32_t wsum[kCsrThreads / 64u];
+    auto &tkey = T.tkey;
+    auto &tfirst = T.tfirst;
+    auto &gid_of = T.gid_of;
+    auto &gstart = T.gstart;
+    auto &fill = T.fill;
+    auto &seg = T.seg;
+    auto &wsum = T.wsum;
     const uint32_t tid = threadIdx.x;
-    for (uint32_t h = tid; h < kHashSlots; h += kCsrThreads) {
-        tkey[h] = 0ull;
-        tfirst[h] = UINT32_MAX;
-    }
-    for (uint32_t g = tid; g < kMaxCsrPairs; g += kCsrThreads) {
-        gstart[g] = 0u;
-        fill[g] = 0u;
-    }
-    __syncthreads();
 
     uint64_t key[2];
     uint32_t slot[2] = {0u, 0u};
@@ -169,8 +183,11 @@ __global__ __launch_bounds__(kCsrThreads) void group_csr_kernel(pulsar_expert_pt
                                                                uint32_t *__restrict__ pairs,
                                                                const pulsar_expert_ptrs *__restrict__ ptrs,
                                                                uint32_t n, uint32_t n_used, uint32_t max_groups) {
+    __shared__ CsrLds T;
+    csr_clear(T);
+    __syncthreads();
     csr_build(
-            gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs[i].gate; },
+            T, gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs[i].gate; },
             [&](uint32_t i) { return ptrs[i]; }, n, n_used, max_groups);
 }
 
@@ -214,6 +231,10 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
     const uint32_t tpw = 64u / lpt, g0 = lane & ~(lpt - 1u), kk = lane - g0;
     const uint64_t gmask = lpt == 64u ? ~0ull : (1ull << lpt) - 1ull;
     const uint32_t kNegInf = score_key(-INFINITY);
+    // the CSR tables are cleared first (the barrier before the build orders
+    // it), while the logits loads are in flight
+    __shared__ CsrLds T;
+    csr_clear(T);
     for (uint32_t tb = wave * tpw; tb < n_tok; tb += (kCsrThreads / 64u) * tpw) {
         const uint32_t t = tb + lane / lpt;
         const bool t_ok = t < n_tok;
@@ -317,7 +338,7 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
         return e >= -1 ? bank_ptrs(bank, n_expert, e) : shared.p[-2 - e];
     };
     csr_build(
-            gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs_of(i).gate; }, ptrs_of,
+            T, gptrs, starts, pairs, [&](uint32_t i) { return (uint64_t)(uintptr_t)ptrs_of(i).gate; }, ptrs_of,
             n_tok * n_slots, n_slots, max_groups);
 }
 
@@ -364,7 +385,9 @@ extern "C" int pulsar_moe_route_group(void *selected, void *weights, void *ptrs,
     pk::SharedSlots sh = {};
     for (uint32_t s = 0; s < n_shared; s++) sh.p[s] = shared[s];
     // lanes per token: a power of two holding the token's experts (J per
-    // lane) and its slots, at least 4
+    // lane) and its slots, at least 4 (J = 8 for 128 experts, 16 lanes per
+    // token, measured slower than J = 4 with 32: the longer per-lane scan
+    // costs more than the LDS-routed exchange it saves)
     const uint32_t jl = n_expert <= 256u ? 4u : n_expert <= 512u ? 8u : 16u;
     const uint32_t need = (n_expert + jl - 1u) / jl > n_slots ? (n_expert + jl - 1u) / jl : n_slots;
     uint32_t lpt = 4u;
@@ -375,9 +398,9 @@ extern "C" int pulsar_moe_route_group(void *selected, void *weights, void *ptrs,
                        (pulsar_expert_ptrs *)gptrs, (uint32_t *)starts, (uint32_t *)pairs, (const float *)logits, \
                        (const float *)router_bias, n_expert, k_used, weight_scale, softmax_mode, *bank, sh, n_shared, \
                        n_tok, max_groups, lpt)
-    if (n_expert <= 256u)
+    if (jl == 4u)
         PK_RG(4);
-    else if (n_expert <= 512u)
+    else if (jl == 8u)
         PK_RG(8);
     else
         PK_RG(16);
