@@ -130,6 +130,12 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
     // latency overlaps that work. A NULL expert reads the token's mid row
     // instead (in bounds: a weight row is shorter than 4 bytes per value)
     // and is not used.
+    // the slot records are requested first (every thread, clamped index: a
+    // load under a branch would be waited for right there) and stored to
+    // LDS after the mid rows are quantized, so the two round trips overlap
+    const uint32_t s_mine = threadIdx.x < n_used ? threadIdx.x : n_used - 1u;
+    const pulsar_expert_ptrs p_mine = ptrs[(uint64_t)token * n_used + s_mine];
+    const float w_mine = slot_w ? slot_w[(uint64_t)token * n_used + s_mine] : 0.0f;
     typename Fmt<Q>::W w_first[UPLMAX];
     if constexpr (NPL == 0) {
         const uint32_t ks = wave < n_pass * n_used ? wave : 0u;
@@ -157,9 +163,9 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
             if (blk < n_blk) quantize_vals_wave<16u, 272u>(v[i], acts_lds + blk * kActLdsPitch);
         }
     }
-    for (uint32_t s = threadIdx.x; s < n_used; s += blockDim.x) {
-        p_l[s] = ptrs[(uint64_t)token * n_used + s];
-        w_l[s] = slot_w ? slot_w[(uint64_t)token * n_used + s] : 0.0f;
+    if (threadIdx.x < n_used) {
+        p_l[threadIdx.x] = p_mine;
+        w_l[threadIdx.x] = w_mine;
     }
     __syncthreads();
     const uint32_t act_bytes = mid_blocks * kActLdsPitch;

@@ -288,6 +288,7 @@ static uint32_t grouped_pmax(uint32_t blocks) {
 }
 
 // Deterministic slot reduce (pulsar_kernels.cu:2791-2806).
+constexpr uint32_t kSumBatch = 8;
 __global__ __launch_bounds__(256) void slot_sum_kernel(float *__restrict__ out,
                                                        const float *__restrict__ partial,
                                                        uint32_t out_dim, uint32_t n_used,
@@ -297,7 +298,15 @@ __global__ __launch_bounds__(256) void slot_sum_kernel(float *__restrict__ out,
     const uint64_t token = gid / out_dim;
     const uint64_t row = gid - token * out_dim;
     float acc = 0.0f;
-    for (uint32_t s = 0; s < n_used; s++) acc += partial[(token * n_used + s) * out_dim + row];
+    for (uint32_t s0 = 0; s0 < n_used; s0 += kSumBatch) {  // a batch's loads issued before its adds
+        float pv[kSumBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kSumBatch; j++)
+            pv[j] = partial[(token * n_used + (s0 + j < n_used ? s0 + j : n_used - 1u)) * out_dim + row];
+#pragma unroll
+        for (uint32_t j = 0; j < kSumBatch; j++)
+            if (s0 + j < n_used) acc += pv[j];
+    }
     out[gid] = acc;
 }
 

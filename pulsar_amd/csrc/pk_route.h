@@ -54,9 +54,11 @@ PK_DEV uint32_t wave_max_u32(uint32_t v) {
 // -inf. Winner number k lands in lane k % 64, slot k / 64 of win / wprob
 // (index, or -1 when every score is NaN; its prob, the raw logit in mode
 // 2). `sum` is the sequential sum of the winners' probs, `wmax` their max.
-template <uint32_t J>
+// KW record slots per lane hold winners 0 .. 64 KW - 1 (KW = 1 for callers
+// with k_used <= 64: one select per round instead of J).
+template <uint32_t J, uint32_t KW = J>
 PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uint32_t k_used, uint32_t mode,
-                      int32_t (&win)[J], float (&wprob)[J], float &sum, float &wmax) {
+                      int32_t (&win)[KW], float (&wprob)[KW], float &sum, float &wmax) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t kNegInf = score_key(-INFINITY);
     uint32_t key[J];
@@ -74,10 +76,13 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
         bias_l[j] = bsrc[ec];
     }
 #pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        const uint32_t e = lane * J + j;
+    for (uint32_t j = 0; j < KW; j++) {
         win[j] = -1;
         wprob[j] = 0.0f;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        const uint32_t e = lane * J + j;
         if (e < n_expert) {
             const float raw = raw_l[j];
             const float p = mode == 1u ? raw : router_sigmoid(raw);
@@ -122,7 +127,7 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
         lane_best();
         const bool rec = lane == (k & 63u);
 #pragma unroll
-        for (uint32_t j = 0; j < J; j++) {
+        for (uint32_t j = 0; j < KW; j++) {
             win[j] = rec && j == (k >> 6) ? w_e : win[j];
             wprob[j] = rec && j == (k >> 6) ? w_p : wprob[j];
         }
@@ -139,10 +144,10 @@ PK_DEV void topk_wave(const float *lg, const float *bias, uint32_t n_expert, uin
 template <uint32_t J>
 PK_DEV void route_lane(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used, float scale,
                        uint32_t mode, int32_t &e, float &w) {
-    int32_t win[J];
-    float wprob[J];
+    int32_t win[1];
+    float wprob[1];
     float sum, wmax;
-    topk_wave<J>(lg, rbias, n_expert, k_used, mode, win, wprob, sum, wmax);
+    topk_wave<J, 1>(lg, rbias, n_expert, k_used, mode, win, wprob, sum, wmax);
     // winner k sits in lane k, slot 0
     const uint32_t lane = threadIdx.x & 63u;
     if (mode == 1u) {
