@@ -438,6 +438,13 @@ def cpu_info() -> dict:
         info["model"] = kv.get("Model name", info["model"])
         if "Core(s) per socket" in kv and "Socket(s)" in kv:
             info["physical_cores"] = int(kv["Core(s) per socket"]) * int(kv["Socket(s)"])
+        # a virtualised host often reports only "AMD EPYC": family / model /
+        # stepping name the generation (family 25 = Zen 3 / 4, 26 = Zen 5)
+        info["family_model_stepping"] = "/".join(kv.get(k, "?") for k in ("CPU family", "Model", "Stepping"))
+        flags = set(kv.get("Flags", "").split())
+        info["simd"] = [f for f in ("avx2", "avx512f", "avx512_vnni", "avx512_bf16", "avx_vnni") if f in flags]
+        if "L3 cache" in kv:
+            info["l3"] = kv["L3 cache"]
     except (OSError, ValueError, subprocess.SubprocessError):
         pass
     if info["model"] == "unknown":
@@ -511,6 +518,9 @@ def cpu_baseline(seconds: float, ctx) -> dict:
         "avx2": oracle.avx2_supported(),
         "lane_default": lane,
         "cpu_model": info["model"],
+        "cpu_family_model_stepping": info.get("family_model_stepping"),
+        "cpu_simd": info.get("simd"),
+        "cpu_l3": info.get("l3"),
         "physical_cores": info["physical_cores"],
         "logical_cpus_visible": info["logical_cpus"],
         "threads_available": avail,

@@ -471,3 +471,19 @@ def test_grouped_every_format(dev, q):
     want = oracle.moe_down(hptrs, midq, L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, q)
     err = np.abs(down(out).astype(np.float64) - want)
     assert (err <= down_bound(L, midq)).all(), f"grouped down: max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("n_used", [1, 8, 9, 16])
+def test_slot_sum_batches_exact(dev, n_used):
+    """moe_slot_sum loads its slots in batches of 8; the sum stays the
+    reference's slot-order float sum from +0 (cu:2791-2806), bit for bit,
+    across a batch boundary and a partial last batch."""
+    n_tok, out_dim = 3, 1000
+    r = np.random.default_rng(n_used)
+    p = (r.standard_normal((n_tok, n_used, out_dim)) * 10.0 ** r.integers(-3, 4, (n_tok, n_used, 1))).astype(np.float32)
+    want = np.zeros((n_tok, out_dim), np.float32)
+    for s in range(n_used):
+        want += p[:, s]
+    out = zeros_f32((n_tok, out_dim))
+    K.moe_slot_sum(out, up_f32(p.reshape(n_tok * n_used, out_dim)), out_dim, n_used, n_tok)
+    assert np.array_equal(down(out).view(np.uint32), want.view(np.uint32))
