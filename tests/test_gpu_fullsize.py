@@ -413,3 +413,61 @@ def test_grouped_row_tiles_partial_last_block(dev, quant, stage):
                 v, a = oracle.rows_dot(mats[0][e], rb, n_rows, xq[so:so + 1], k_dim, 1, quant, THREADS)
                 err = np.abs(got[so].astype(np.float64) - v[0])
                 assert (err <= TOL_REL * a[0] + 1e-30).all(), (t, s, float(err.max()))
+
+
+@pytest.mark.parametrize("quant,stage", [(QUANT_Q2_K, "pair"), (QUANT_Q2_K, "down"), (QUANT_IQ2_XXS, "pair"),
+                                         (QUANT_IQ2_XXS, "down"), (fm.QUANT_MXFP4, "pair"),
+                                         (fm.QUANT_MXFP4, "down"), (QUANT_Q4_K, "pair")],
+                         ids=lambda v: fm.NAMES.get(v, v) if isinstance(v, int) else v)
+def test_grouped_tile_sizes(dev, quant, stage):
+    """Groups of exactly 1, 2, 3, 4, 5, 6, 16 and 17 pairs: the grouped MFMA
+    kernel's epilogue for tiles of at most four pairs (results moved across
+    lanes) and for larger tiles, and groups that take a second pair tile
+    (the tile holds fewer pairs than 16 or 17 at these widths), against the
+    oracle's row dots; 200 rows leave a partial row block."""
+    sizes = [1, 2, 3, 4, 5, 6, 16, 17]
+    n_used, n_rows = 6, 200
+    n_pairs = sum(sizes)
+    n_tok = n_pairs // n_used
+    assert n_tok * n_used == n_pairs
+    k_dim = (1024 if stage == "pair" else 512) if quant != fm.QUANT_MXFP4 else 960
+    rng = np.random.default_rng(7 + quant)
+    E = len(sizes)
+    flat = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)])
+    sel = rng.permutation(flat).reshape(n_tok, n_used)
+    rb = row_bytes(quant, k_dim)
+    mats = [synth.quant_matrix(quant, E * n_rows, k_dim, synth.rng_for(quant, f"ts{stage}{m}")).reshape(E, n_rows, rb)
+            for m in range(2 if stage == "pair" else 1)]
+    devs = [up(np.concatenate([m.reshape(-1), np.zeros(256, np.uint8)])) for m in mats]
+    w = rng.uniform(0.1, 1.0, (n_tok, n_used)).astype(np.float32)
+    n_act = n_tok if stage == "pair" else n_tok * n_used
+    xq = oracle.quantize_q8_k(rng.standard_normal((n_act, k_dim)).astype(np.float32))
+    ids, starts, pairs = synth.csr_by_expert(sel, n_used)
+    assert sorted(np.diff(starts).tolist()) == sorted(sizes)
+    entries = []
+    for e in ids:
+        a = [d.data_ptr() + int(e) * n_rows * rb for d in devs]
+        entries.append((a[0], a[-1], 0) if stage == "pair" else (0, 0, a[0]))
+    gptrs = up(K.expert_ptrs(entries))
+    out = zeros_f32((n_tok * n_used, n_rows))
+    if stage == "pair":
+        K.moe_pair_swiglu_grouped(out, gptrs, up(starts), up(pairs), up_f32(w), up(xq), k_dim, n_rows, n_used,
+                                  len(ids), rb, quant, 0)
+    else:
+        K.moe_down_grouped(out, gptrs, up(starts), up(pairs), up(xq), k_dim, n_rows, n_used, len(ids), rb, quant)
+    got = down(out)
+    for t in range(n_tok):
+        for s in range(n_used):
+            e, so = int(sel[t, s]), t * n_used + s
+            if stage == "pair":
+                g, ag = oracle.rows_dot(mats[0][e], rb, n_rows, xq[t:t + 1], k_dim, 1, quant, THREADS)
+                u, au = oracle.rows_dot(mats[1][e], rb, n_rows, xq[t:t + 1], k_dim, 1, quant, THREADS)
+                want = np.array([oracle.glu(float(a), float(b), 0) * w[t, s] for a, b in zip(g[0], u[0])])
+                bound = TOL_REL * w[t, s] * (1.5 * (np.abs(u[0]) + 1) * ag[0] + (np.abs(g[0]) + 1) * au[0])
+                bound += 4e-7 * np.abs(want) + 1e-30
+                err = np.abs(got[so].astype(np.float64) - want)
+                assert (err <= bound).all(), (t, s, e, float(err.max()))
+            else:
+                v, a = oracle.rows_dot(mats[0][e], rb, n_rows, xq[so:so + 1], k_dim, 1, quant, THREADS)
+                err = np.abs(got[so].astype(np.float64) - v[0])
+                assert (err <= TOL_REL * a[0] + 1e-30).all(), (t, s, e, float(err.max()))
