@@ -146,7 +146,8 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
                                 : (const uint8_t *)(mid + (uint64_t)token * n_used * mid_dim);
         load_row_w<Q, UPLMAX>(as_global(src), rg, w_first);
     }
-    // the wave's mid blocks blk = wave + nw i, loaded four at a time before use
+    // the wave's mid blocks blk = wave + nw i, loaded four at a time before
+    // use and quantized two at a time (their reductions interleave)
     for (uint32_t base = wave; base < n_blk; base += 4u * nw) {
         float v[4][4];
 #pragma unroll
@@ -155,12 +156,17 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
             if (blk < n_blk) {
                 const uint32_t s = blk / mid_blocks, b = blk - s * mid_blocks;
                 load_block4(mid + ((uint64_t)token * n_used + s) * mid_dim, mid_dim, b, v[i]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[i][j] = 0.0f;
             }
         }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
+        for (uint32_t i = 0; i < 4; i += 2) {
             const uint32_t blk = base + nw * i;
-            if (blk < n_blk) quantize_vals_wave<16u, 272u>(v[i], acts_lds + blk * kActLdsPitch);
+            if (blk < n_blk)
+                quantize_vals_wave2<16u, 272u>(v[i], v[i + 1], acts_lds + blk * kActLdsPitch,
+                                               acts_lds + (blk + nw) * kActLdsPitch, blk + nw < n_blk);
         }
     }
     if (threadIdx.x < n_used) {

@@ -29,32 +29,65 @@ PK_DEV void load_block4(const float *xr, uint32_t in_dim, uint32_t b, float (&v)
     }
 }
 
-template <uint32_t QOFF, uint32_t BOFF>
-PK_DEV void quantize_vals_wave(const float (&v)[4], uint8_t *ob) {
-    const uint32_t lane = threadIdx.x & 63u;
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = wave_max(am);
-    uint32_t packed = 0;
-    int32_t s4 = 0;
-    float d = 0.0f;
-    if (am != 0.0f) {
-        d = am / 127.0f;
-        const float inv = 127.0f / am;
+// One lane's share of a block: its 4 quants packed, their sum, and the
+// block's d. No branch on amax == 0: there inv = 127 / 0 = inf and every
+// x * inv is 0 * inf = NaN, which the saturating conversion maps to 0, the
+// quants of an all-zero block (so two blocks can share one instruction
+// stream).
+PK_DEV void quantize_lane(const float (&v)[4], float am, uint32_t &packed, int32_t &s4, float &d) {
+    d = am / 127.0f;
+    const float inv = 127.0f / am;
+    packed = 0;
+    s4 = 0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            float q = roundf(v[j] * inv);
-            // Rust's saturating `as i8` maps NaN (0 * inf when 127/amax
-            // overflows) to 0
-            q = q != q ? 0.0f : fminf(fmaxf(q, -127.0f), 127.0f);
-            const int32_t qi = (int32_t)q;
-            s4 += qi;
-            packed |= ((uint32_t)qi & 0xffu) << (8 * j);
-        }
+    for (int j = 0; j < 4; j++) {
+        float q = roundf(v[j] * inv);
+        // Rust's saturating `as i8` maps NaN (0 * inf when 127/amax
+        // overflows or amax is 0) to 0
+        q = q != q ? 0.0f : fminf(fmaxf(q, -127.0f), 127.0f);
+        const int32_t qi = (int32_t)q;
+        s4 += qi;
+        packed |= ((uint32_t)qi & 0xffu) << (8 * j);
     }
+}
+
+template <uint32_t QOFF, uint32_t BOFF>
+PK_DEV void store_quant(uint8_t *ob, uint32_t packed, int32_t s4, float d) {
+    const uint32_t lane = threadIdx.x & 63u;
     *(uint32_t *)(ob + QOFF + 4 * lane) = packed;
-    s4 = group_sum<4>(s4);
     if ((lane & 3u) == 0u) *(int16_t *)(ob + BOFF + 2 * (lane >> 2)) = (int16_t)s4;
     if (lane == 0) *(float *)ob = d;
+}
+
+template <uint32_t QOFF, uint32_t BOFF>
+PK_DEV void quantize_vals_wave(const float (&v)[4], uint8_t *ob) {
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = wave_max(am);
+    uint32_t packed;
+    int32_t s4;
+    float d;
+    quantize_lane(v, am, packed, s4, d);
+    s4 = group_sum<4>(s4);
+    store_quant<QOFF, BOFF>(ob, packed, s4, d);
+}
+
+// Two blocks at once (the same arithmetic; their reductions interleave).
+// The second block is stored only when has1.
+template <uint32_t QOFF, uint32_t BOFF>
+PK_DEV void quantize_vals_wave2(const float (&v0)[4], const float (&v1)[4], uint8_t *ob0, uint8_t *ob1, bool has1) {
+    float a0 = fmaxf(fmaxf(fabsf(v0[0]), fabsf(v0[1])), fmaxf(fabsf(v0[2]), fabsf(v0[3])));
+    float a1 = fmaxf(fmaxf(fabsf(v1[0]), fabsf(v1[1])), fmaxf(fabsf(v1[2]), fabsf(v1[3])));
+    a0 = wave_max(a0);
+    a1 = wave_max(a1);
+    uint32_t p0, p1;
+    int32_t s0, s1;
+    float d0, d1;
+    quantize_lane(v0, a0, p0, s0, d0);
+    quantize_lane(v1, a1, p1, s1, d1);
+    s0 = group_sum<4>(s0);
+    s1 = group_sum<4>(s1);
+    store_quant<QOFF, BOFF>(ob0, p0, s0, d0);
+    if (has1) store_quant<QOFF, BOFF>(ob1, p1, s1, d1);
 }
 
 template <uint32_t QOFF, uint32_t BOFF>

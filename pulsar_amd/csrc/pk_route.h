@@ -265,11 +265,11 @@ template <uint32_t J>
 PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expert, uint32_t k_used,
                             float scale, uint32_t mode, const pulsar_expert_bank &bank, const SharedSlots &shared,
                             uint32_t slot) {
-    int32_t e;
-    float wk;
-    route_lane<J>(lg, rbias, n_expert, k_used, scale, mode, e, wk);
     SlotRoute r;
-    if (slot < k_used) {
+    if (slot < k_used) {  // wave-uniform: a shared slot needs no routing
+        int32_t e;
+        float wk;
+        route_lane<J>(lg, rbias, n_expert, k_used, scale, mode, e, wk);
         r.e = __builtin_amdgcn_readlane(e, (int)slot);
         r.w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), (int)slot));
         r.p = bank_ptrs(bank, n_expert, r.e);
