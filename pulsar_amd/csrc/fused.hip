@@ -125,31 +125,15 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t pass0 = blockIdx.x * n_pass;
-    // Unstaged rows: the wave's first (pass, slot) item has its weights
-    // requested before the mid rows are loaded and quantized, so their HBM
-    // latency overlaps that work. A NULL expert reads the token's mid row
-    // instead (in bounds: a weight row is shorter than 4 bytes per value)
-    // and is not used.
     // the slot records are requested first (every thread, clamped index: a
     // load under a branch would be waited for right there) and stored to
     // LDS after the mid rows are quantized, so the two round trips overlap
     const uint32_t s_mine = threadIdx.x < n_used ? threadIdx.x : n_used - 1u;
     const pulsar_expert_ptrs p_mine = ptrs[(uint64_t)token * n_used + s_mine];
     const float w_mine = slot_w ? slot_w[(uint64_t)token * n_used + s_mine] : 0.0f;
-    typename Fmt<Q>::W w_first[UPLMAX];
-    if constexpr (NPL == 0) {
-        const uint32_t ks = wave < n_pass * n_used ? wave : 0u;
-        const uint32_t k = ks / n_used, s = ks - k * n_used;
-        const uint32_t row = (pass0 + k) * rpp + rg.rip;
-        const uint8_t *dp = (const uint8_t *)ptrs[(uint64_t)token * n_used + s].down;
-        const uint8_t *src = dp ? dp + (uint64_t)(row < out_dim ? row : 0u) * row_bytes
-                                : (const uint8_t *)(mid + (uint64_t)token * n_used * mid_dim);
-        load_row_w<Q, UPLMAX>(as_global(src), rg, w_first);
-    }
     // the wave's mid blocks blk = wave + nw i, loaded four at a time before
     // use and quantized two at a time (their reductions interleave)
-    for (uint32_t base = wave; base < n_blk; base += 4u * nw) {
-        float v[4][4];
+    auto load_batch = [&](uint32_t base, float (&v)[4][4]) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
             const uint32_t blk = base + nw * i;
@@ -161,6 +145,8 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
                 for (int j = 0; j < 4; j++) v[i][j] = 0.0f;
             }
         }
+    };
+    auto quantize_batch = [&](uint32_t base, const float (&v)[4][4]) {
 #pragma unroll
         for (uint32_t i = 0; i < 4; i += 2) {
             const uint32_t blk = base + nw * i;
@@ -168,6 +154,30 @@ __global__ __launch_bounds__(1024) void moe_down_f32_kernel(
                 quantize_vals_wave2<16u, 272u>(v[i], v[i + 1], acts_lds + blk * kActLdsPitch,
                                                acts_lds + (blk + nw) * kActLdsPitch, blk + nw < n_blk);
         }
+    };
+    // the first batch is requested before the first weight row, whose
+    // address waits for the slot record (a round trip of its own). Unstaged
+    // rows: the wave's first (pass, slot) item then has its weights in
+    // flight while the mid rows are quantized. A NULL expert reads the
+    // token's mid row instead (in bounds: a weight row is shorter than 4
+    // bytes per value) and is not used.
+    float v0[4][4];
+    load_batch(wave, v0);
+    typename Fmt<Q>::W w_first[UPLMAX];
+    if constexpr (NPL == 0) {
+        const uint32_t ks = wave < n_pass * n_used ? wave : 0u;
+        const uint32_t k = ks / n_used, s = ks - k * n_used;
+        const uint32_t row = (pass0 + k) * rpp + rg.rip;
+        const uint8_t *dp = (const uint8_t *)ptrs[(uint64_t)token * n_used + s].down;
+        const uint8_t *src = dp ? dp + (uint64_t)(row < out_dim ? row : 0u) * row_bytes
+                                : (const uint8_t *)(mid + (uint64_t)token * n_used * mid_dim);
+        load_row_w<Q, UPLMAX>(as_global(src), rg, w_first);
+    }
+    quantize_batch(wave, v0);
+    for (uint32_t base = wave + 4u * nw; base < n_blk; base += 4u * nw) {
+        float v[4][4];
+        load_batch(base, v);
+        quantize_batch(base, v);
     }
     if (threadIdx.x < n_used) {
         p_l[threadIdx.x] = p_mine;
