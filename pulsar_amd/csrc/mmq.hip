@@ -186,11 +186,15 @@ PK_DEV uint32_t pair_sum_bytes(uint4 b, bool high) {
 // RT C waves. Per chunk the rows' super-blocks (row-contiguous 16-byte
 // copies) and the tokens' q8 values (+ bsums for Q4_K, + d) are staged in
 // LDS; wave (rt, sb) decodes row tile rt, super-block sb of the chunk once
-// and multiplies it with all NT token tiles. The next chunk's loads are
-// issued before the current chunk is decoded; every thread issues every
-// load (clamped, stored or not), so the waits count exactly one chunk.
+// and multiplies it with all NT token tiles. The loads of D chunks are in
+// flight at once, in D register buffers: chunks are taken in groups of D,
+// and as buffer d is moved to LDS, the next group's chunk d is requested
+// into it. Every thread issues every load (clamped, stored or not) in the
+// same order in the first group and the loop, so each wait counts exactly
+// the D - 1 chunks behind the one needed; only the last group's requests
+// past the end of K (clamped to its last super-block) are wasted.
 // The C partials of a row tile are added in wave order (deterministic).
-template <uint32_t Q, uint32_t RT, uint32_t C, uint32_t NT>
+template <uint32_t Q, uint32_t RT, uint32_t C, uint32_t NT, uint32_t D>
 __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict__ out, const uint8_t *__restrict__ w,
                                                                const pulsar_block_q8_K *__restrict__ xq, uint32_t nb,
                                                                uint32_t out_dim, uint32_t n_tok, uint64_t row_bytes) {
@@ -248,29 +252,31 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
         ysb[m] = sb;
         ydst[m] = f < TOK * C ? sb * TOK + t : UINT32_MAX;
     }
-    uint4 wreg[kWL], areg[kAL];
-    uint32_t yreg[kYL];
-    auto gload = [&](uint32_t kb) {
+    uint4 wreg[D][kWL], areg[D][kAL];
+    uint32_t yreg[D][kYL];
+    // buffer d (a constant once the callers' loops are unrolled) <- chunk at kb
+    auto gload = [&](uint32_t kb, uint32_t d) {
 #pragma unroll
         for (uint32_t m = 0; m < kWL; m++)
-            wreg[m] = ldw128(wsrc[m] + (uint64_t)(kb + wsb[m] < nb ? kb + wsb[m] : nb - 1u) * F::kSb);
+            wreg[d][m] = ldw128(wsrc[m] + (uint64_t)(kb + wsb[m] < nb ? kb + wsb[m] : nb - 1u) * F::kSb);
 #pragma unroll
         for (uint32_t m = 0; m < kAL; m++)
-            areg[m] = ld128(asrc[m] + (uint64_t)(kb + asb[m] < nb ? kb + asb[m] : nb - 1u) * 292u);
+            areg[d][m] = ld128(asrc[m] + (uint64_t)(kb + asb[m] < nb ? kb + asb[m] : nb - 1u) * 292u);
 #pragma unroll
         for (uint32_t m = 0; m < kYL; m++)
-            yreg[m] = ld32(ysrc[m] + (uint64_t)(kb + ysb[m] < nb ? kb + ysb[m] : nb - 1u) * 292u);
+            yreg[d][m] = ld32(ysrc[m] + (uint64_t)(kb + ysb[m] < nb ? kb + ysb[m] : nb - 1u) * 292u);
     };
-    auto lstore = [&]() {
+    auto lstore = [&](uint32_t d) {
 #pragma unroll
         for (uint32_t m = 0; m < kWL; m++)
-            if ((m + 1u) * NTH <= kWP || wdst[m] != UINT32_MAX) *(uint4 *)(wl + wdst[m]) = wreg[m];
+            if ((m + 1u) * NTH <= kWP || wdst[m] != UINT32_MAX) *(uint4 *)(wl + wdst[m]) = wreg[d][m];
 #pragma unroll
         for (uint32_t m = 0; m < kAL; m++)
-            if ((m + 1u) * NTH <= kAP || adst[m] != UINT32_MAX) *(uint4 *)(lds + adst[m]) = areg[m];
+            if ((m + 1u) * NTH <= kAP || adst[m] != UINT32_MAX) *(uint4 *)(lds + adst[m]) = areg[d][m];
 #pragma unroll
         for (uint32_t m = 0; m < kYL; m++)
-            if ((m + 1u) * NTH <= TOK * C || ydst[m] != UINT32_MAX) yl[ydst[m]] = __builtin_bit_cast(float, yreg[m]);
+            if ((m + 1u) * NTH <= TOK * C || ydst[m] != UINT32_MAX)
+                yl[ydst[m]] = __builtin_bit_cast(float, yreg[d][m]);
     };
 
     const uint32_t rt = wave / C, sbw = wave % C;
@@ -405,19 +411,31 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
             }
         }
     };
-    gload(0);
-    uint32_t kb = 0;
-    for (; kb + C < nb; kb += C) {
-        lstore();
-        __syncthreads();
-        gload(kb + C);  // in flight while this chunk is decoded
-        chunk(kb);
-        __syncthreads();
+    const uint32_t n_grp = (nb + C * D - 1u) / (C * D);  // groups of D chunks
+#pragma unroll
+    for (uint32_t d = 0; d < D; d++) gload(d * C, d);
+    uint32_t g = 0;
+    for (; g + 1u < n_grp; g++) {
+#pragma unroll
+        for (uint32_t d = 0; d < D; d++) {
+            const uint32_t kb = (g * D + d) * C;
+            lstore(d);
+            __syncthreads();
+            gload(kb + D * C, d);  // in flight while this chunk and the next D - 1 are decoded
+            chunk(kb);
+            __syncthreads();
+        }
     }
-    lstore();  // the last chunk: nothing left to prefetch
-    __syncthreads();
-    chunk(kb);
-    __syncthreads();
+#pragma unroll
+    for (uint32_t d = 0; d < D; d++) {  // the last group: nothing left to request
+        const uint32_t kb = (g * D + d) * C;
+        if (kb < nb) {
+            lstore(d);
+            __syncthreads();
+            chunk(kb);
+            __syncthreads();
+        }
+    }
     // partials [wave][row][token] over the activation area (all reads of it are done)
     float *part = (float *)al;
 #pragma unroll
@@ -443,24 +461,37 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
 #ifndef PK_GEMM_NT2
 #define PK_GEMM_NT2 32u
 #endif
+// chunks in flight (cold weights, 16 tokens): 32-row tiles over Q6_K 8192 x
+// 4096 13.0 / 12.5 / 13.7 us at 1 / 2 / 4 (all requested at once, the last
+// chunk's data comes with the first: the decodes then run back to back);
+// 16-row tiles over Q4_K 4096 x 4096 7.7 / 7.8 / 9.3 us
+#ifndef PK_GEMM_D_NT2
+#define PK_GEMM_D_NT2 1u
+#endif
+#ifndef PK_GEMM_D_R16
+#define PK_GEMM_D_R16 1u
+#endif
+#ifndef PK_GEMM_D_R32
+#define PK_GEMM_D_R32 2u
+#endif
 
 template <uint32_t Q>
 static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *xq, uint32_t nb, uint32_t out_dim,
                          uint32_t n_tok, uint64_t row_bytes) {
-#define PK_GEMM(RT, C, NT)                                                                                   \
-    hipLaunchKernelGGL((mmq_gemm_kernel<Q, RT, C, NT>), dim3((n_tok + 16u * NT - 1u) / (16u * NT),            \
-                                                             (out_dim + 16u * RT - 1u) / (16u * RT)),          \
+#define PK_GEMM(RT, C, NT, D)                                                                                \
+    hipLaunchKernelGGL((mmq_gemm_kernel<Q, RT, C, NT, D>), dim3((n_tok + 16u * NT - 1u) / (16u * NT),         \
+                                                                (out_dim + 16u * RT - 1u) / (16u * RT)),       \
                        dim3(64 * RT * C), 0, pk::stream(), out, w, xq, nb, out_dim, n_tok, row_bytes)
     // below 8192 rows a 32-row tile leaves CUs idle (4096 rows: 128 blocks);
     // 16-row tiles with 8 super-blocks per chunk measured fastest there
     // (Q4_K 4096 x 4096, 16 tokens: 8.7 -> 6.9 us), 32-row tiles with 4
     // above (Q6_K 8192 x 4096: 11.8 us; 16-row tiles 12.9-14.0 us)
     if (n_tok >= PK_GEMM_NT2)
-        PK_GEMM(2, 2, 2);
+        PK_GEMM(2, 2, 2, PK_GEMM_D_NT2);
     else if (out_dim < 8192u)
-        PK_GEMM(1, 8, 1);
+        PK_GEMM(1, 8, 1, PK_GEMM_D_R16);
     else
-        PK_GEMM(2, 4, 1);
+        PK_GEMM(2, 4, 1, PK_GEMM_D_R32);
 #undef PK_GEMM
     return launch_ok("matmul_kq gemm launch");
 }
@@ -723,13 +754,13 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot + c) : UINT32_MAX;
     }
     uint8_t *wl_w = &wl[wave][0];
-    const uint32_t act_bytes = k_blocks * kActLdsPitch;
+    const uint32_t act_bytes = act_row_pitch(k_blocks);
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
         if (t0 != s0) __syncthreads();  // the previous tile's activations are consumed
         if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
         __syncthreads();
-        stage_q8_rows<2>(acts_lds, m, k_blocks, [&](uint32_t j) {
+        stage_q8_rows<2>(acts_lds, m, k_blocks, act_bytes, [&](uint32_t j) {
             const uint32_t pr = pr_l[j];
             return act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) * k_blocks;
         });
@@ -1060,7 +1091,7 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
         return -1;
     const uint32_t k_blocks = (k_dim + 255u) / 256u;
     const uint32_t lim = quant == PULSAR_QUANT_MXFP4 ? k_dim / 32u : k_blocks;
-    const uint32_t per_pair = k_blocks * kActLdsPitch;
+    const uint32_t per_pair = act_row_pitch(k_blocks);
     // MXFP4 layers route many pairs to each expert (gpt-oss: 64 tokens x 4 of
     // 32 experts), so their tiles take more pairs per weight pass
     const uint32_t budget = quant == PULSAR_QUANT_MXFP4 ? kGqActLdsMx : kGqActLds;

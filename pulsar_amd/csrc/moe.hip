@@ -131,7 +131,7 @@ PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const uint32_t *pairs
                             const pulsar_block_q8_K *src, uint32_t blocks, uint32_t n_used) {
     for (uint32_t j = threadIdx.x; j < np; j += blockDim.x) pr_l[j] = pairs[c0 + j];
     __syncthreads();
-    stage_q8_rows<2>(acts, np, blocks, [&](uint32_t j) {
+    stage_q8_rows<2>(acts, np, blocks, blocks * kActLdsPitch, [&](uint32_t j) {
         const uint32_t pr = pr_l[j];
         const uint64_t row = DOWN ? (uint64_t)(pr >> 4) * n_used + (pr & 15u) : (uint64_t)(pr >> 4);
         return src + row * blocks;

@@ -117,6 +117,15 @@ PK_DEV void load_act(const pulsar_block_q8_K *xq_row, uint32_t g, Act &a) {
 // (k == 0 ? 0 : 4k + 12).
 constexpr uint32_t kActLdsPitch = 304u;
 PK_DEV uint32_t act_lds_offset(uint32_t k) { return k == 0 ? 0u : 4u * k + 12u; }
+// Bytes between consecutive staged rows that the 16 lanes of an MFMA operand
+// read together (one row per lane): the row's blocks plus 16 bytes when their
+// count is even. The stride is then 4 (mod 8) dwords, so the 16 rows start in
+// 16 distinct groups of 4 of the LDS's 64 four-byte banks; an even count
+// alone makes it a multiple of 8 dwords (16 blocks: a multiple of 64, every
+// row on the same banks).
+__host__ __device__ inline uint32_t act_row_pitch(uint32_t k_blocks) {
+    return k_blocks * kActLdsPitch + (k_blocks % 2u == 0u ? 16u : 0u);
+}
 
 template <bool ACT_STRIDE32, int BS_MODE>
 PK_DEV void load_act_lds(const uint8_t *row, uint32_t g, Act &a) {

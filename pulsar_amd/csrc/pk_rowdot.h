@@ -95,34 +95,38 @@ PK_DEV void load_row_acts_lds(const uint8_t *row, const RowGeom &rg, Act (&a)[UP
 }
 
 // Block-wide copy of m q8_K rows (k_blocks blocks each) into LDS in the
-// load_act_lds layout; row j comes from the global q8_K row src_row(j).
+// load_act_lds layout, row j at byte j * row_pitch; row j comes from the
+// global q8_K row src_row(j).
 // A block is copied as 16 + 2 16-byte pieces (qs, bsums) and its d, all
 // loads of a batch of B per thread issued before their stores (B trades
 // registers for loads in flight).
 template <uint32_t B, typename RowFn>
-PK_DEV void stage_q8_rows(uint8_t *lds, uint32_t m, uint32_t k_blocks, RowFn src_row) {
+PK_DEV void stage_q8_rows(uint8_t *lds, uint32_t m, uint32_t k_blocks, uint32_t row_pitch, RowFn src_row) {
     const uint32_t per_row = k_blocks * 19u, total = m * per_row;
     for (uint32_t base = threadIdx.x; base < total; base += B * blockDim.x) {
         uint4 v[B];
         uint32_t dst[B];
+        bool is_d[B];
 #pragma unroll
         for (uint32_t u = 0; u < B; u++) {
             const uint32_t it = base + u * blockDim.x;
             dst[u] = UINT32_MAX;
+            is_d[u] = false;
             if (it < total) {
                 const uint32_t j = it / per_row, r = it - j * per_row, sb = r / 19u, c = r - sb * 19u;
                 const uint8_t *src = (const uint8_t *)src_row(j) + (uint64_t)sb * 292u;
                 // pieces 0..15: qs (source 4 + 16c), 16, 17: bsums (260, 276), 18: d (0)
                 const uint32_t so = c < 16u ? 4u + 16u * c : c == 16u ? 260u : c == 17u ? 276u : 0u;
                 const uint32_t dofs = c < 16u ? 16u + 16u * c : c == 16u ? 272u : c == 17u ? 288u : 0u;
-                dst[u] = (j * k_blocks + sb) * kActLdsPitch + dofs;
+                dst[u] = j * row_pitch + sb * kActLdsPitch + dofs;
+                is_d[u] = c == 18u;
                 v[u] = c < 18u ? ld128(src + so) : make_uint4(ld32(src), 0u, 0u, 0u);
             }
         }
 #pragma unroll
         for (uint32_t u = 0; u < B; u++) {
             if (dst[u] == UINT32_MAX) continue;
-            if (dst[u] % kActLdsPitch == 0u)
+            if (is_d[u])
                 *(uint32_t *)(lds + dst[u]) = v[u].x;  // d
             else
                 *(uint4 *)(lds + dst[u]) = v[u];
