@@ -213,7 +213,10 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
     __shared__ __align__(16) uint8_t lds[kWlBytes + kAlBytes + kBlBytes + C * TOK * 4u];
     uint8_t *wl = lds, *al = lds + kWlBytes, *bl = al + kAlBytes;
     float *yl = (float *)(bl + kBlBytes);
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    // the wave index through readfirstlane: known wave-uniform, so branches
+    // on it stay scalar (a masked branch would let one side's loads be in
+    // flight into registers the other side reuses, and force a full wait)
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t i = lane & 15u, kq = lane >> 4;
     const uint32_t t0 = blockIdx.x * TOK, r0 = blockIdx.y * ROWS;
     const uint8_t *xb = (const uint8_t *)xq;
@@ -254,17 +257,25 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
     }
     uint4 wreg[D][kWL], areg[D][kAL];
     uint32_t yreg[D][kYL];
-    // buffer d (a constant once the callers' loops are unrolled) <- chunk at kb
+    // load p of the chunk at kb into buffer d (p, d constants once the
+    // callers' loops are unrolled): the weight pieces, then the q8 values,
+    // then the d values
+    constexpr uint32_t kNL = kWL + kAL + kYL;
+    auto gload_one = [&](uint32_t kb, uint32_t d, uint32_t p) {
+        if (p < kWL) {
+            const uint32_t m = p;
+            wreg[d][m] = ldw128(wsrc[m] + (uint64_t)(kb + wsb[m] < nb ? kb + wsb[m] : nb - 1u) * F::kSb);
+        } else if (p < kWL + kAL) {
+            const uint32_t m = p - kWL;
+            areg[d][m] = ld128(asrc[m] + (uint64_t)(kb + asb[m] < nb ? kb + asb[m] : nb - 1u) * 292u);
+        } else {
+            const uint32_t m = p - kWL - kAL;
+            yreg[d][m] = ld32(ysrc[m] + (uint64_t)(kb + ysb[m] < nb ? kb + ysb[m] : nb - 1u) * 292u);
+        }
+    };
     auto gload = [&](uint32_t kb, uint32_t d) {
 #pragma unroll
-        for (uint32_t m = 0; m < kWL; m++)
-            wreg[d][m] = ldw128(wsrc[m] + (uint64_t)(kb + wsb[m] < nb ? kb + wsb[m] : nb - 1u) * F::kSb);
-#pragma unroll
-        for (uint32_t m = 0; m < kAL; m++)
-            areg[d][m] = ld128(asrc[m] + (uint64_t)(kb + asb[m] < nb ? kb + asb[m] : nb - 1u) * 292u);
-#pragma unroll
-        for (uint32_t m = 0; m < kYL; m++)
-            yreg[d][m] = ld32(ysrc[m] + (uint64_t)(kb + ysb[m] < nb ? kb + ysb[m] : nb - 1u) * 292u);
+        for (uint32_t p = 0; p < kNL; p++) gload_one(kb, d, p);
     };
     auto lstore = [&](uint32_t d) {
 #pragma unroll
@@ -285,8 +296,14 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
     for (uint32_t n = 0; n < NT; n++)
 #pragma unroll
         for (int r = 0; r < 4; r++) acc[n][r] = 0.0f;
-    auto chunk = [&](uint32_t kb) {
-        if (kb + sbw < nb) {
+    // decodes the chunk at kb; hook(st) runs at the start of each of the 8
+    // steps. With one token tile (loads in the hook) a wave past the end of K
+    // decodes its clamped copy too and adds nothing: a branch around the
+    // decode would put the other side's loads on the decode's path, where
+    // their registers force a full wait
+    auto chunk = [&](uint32_t kb, auto hook) {
+        const bool live = kb + sbw < nb;
+        if (NT == 1u || live) {
             const uint8_t *wrow = wl + (rt * 16u + i) * kRowPitch + sbw * kSlot;
             const uint8_t *abase = al + (sbw * TOK + i) * kActPitch + 8u * kq;
             if constexpr (Q == PULSAR_QUANT_Q6_K) {
@@ -298,6 +315,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                     for (int r = 0; r < 4; r++) isum[n][r] = 0;
 #pragma unroll
                 for (int st = 0; st < 8; st++) {
+                    hook((uint32_t)st);
                     const int h = st >> 2, q = st & 3;
                     const uint2 c = MmaQ6K::codes(wv, h, q);
                     const uint2 c_lo = kq < 2 ? c : make_uint2(0u, 0u);
@@ -319,7 +337,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                     const float4 yd4 = lds_f4(yl + sbw * TOK + 16u * n + 4u * kq);
                     const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[n][r] += xd * yd[r] * (float)isum[n][r];
+                    for (int r = 0; r < 4; r++) acc[n][r] = live ? acc[n][r] + xd * yd[r] * (float)isum[n][r] : acc[n][r];
                 }
             } else if constexpr (Q == PULSAR_QUANT_NVFP4) {
                 // step t: block t / 2, 16-value sub-blocks s0 = 2 (t & 1) and
@@ -337,6 +355,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                 const uint32_t nsh = 4u * (kq & 1u);
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
+                    hook((uint32_t)t);
                     const uint8_t *bp = wrow + 36u * (uint32_t)(t >> 1);
                     const uint8_t *sp = bp + 4u + 8u * (2u * (uint32_t)(t & 1) + (kq >> 1));
                     const uint2 c = make_uint2(mxfp4_kv4(*(const uint32_t *)sp >> nsh),
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                     const float4 yd4 = lds_f4(yl + sbw * TOK + 16u * n + 4u * kq);
                     const float yd[4] = {yd4.x, yd4.y, yd4.z, yd4.w};
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[n][r] += yd[r] * f[n][r];
+                    for (int r = 0; r < 4; r++) acc[n][r] = live ? acc[n][r] + yd[r] * f[n][r] : acc[n][r];
                 }
             } else {  // Q4_K, Q5_K
                 using M = MmaKq<Q>;
@@ -375,6 +394,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
                 uint32_t mins[2] = {0u, 0u};
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
+                    hook((uint32_t)t);
                     int32_t sc, mn;
                     Fmt<PULSAR_QUANT_Q4_K>::scale_min(wv.hdr, (uint32_t)t, sc, mn);
                     mins[t >> 2] |= (uint32_t)mn << (8 * (t & 3));
@@ -405,7 +425,8 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int32_t msum = dl[r] + 128 * dh[r];
-                        acc[n][r] += xd * yd[r] * (float)isum[n][r] - xmin * yd[r] * (float)msum;
+                        const float v = xd * yd[r] * (float)isum[n][r] - xmin * yd[r] * (float)msum;
+                        acc[n][r] = live ? acc[n][r] + v : acc[n][r];
                     }
                 }
             }
@@ -421,8 +442,21 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
             const uint32_t kb = (g * D + d) * C;
             lstore(d);
             __syncthreads();
-            gload(kb + D * C, d);  // in flight while this chunk and the next D - 1 are decoded
-            chunk(kb);
+            // the chunk D ahead, in flight while this one and the next D - 1
+            // are decoded. One token tile: its loads spread over the decode's
+            // steps (issued at once, they stall the wave until the memory
+            // pipeline drains); two tiles decode long enough to hide them,
+            // and interleaving would cost them occupancy
+            if constexpr (NT == 1) {
+                chunk(kb, [&](uint32_t st) {
+#pragma unroll
+                    for (uint32_t p = 0; p < kNL; p++)
+                        if (p * 8u / kNL == st) gload_one(kb + D * C, d, p);
+                });
+            } else {
+                gload(kb + D * C, d);
+                chunk(kb, [](uint32_t) {});
+            }
             __syncthreads();
         }
     }
@@ -432,7 +466,7 @@ __global__ __launch_bounds__(64 * RT * C) void mmq_gemm_kernel(float *__restrict
         if (kb < nb) {
             lstore(d);
             __syncthreads();
-            chunk(kb);
+            chunk(kb, [](uint32_t) {});
             __syncthreads();
         }
     }

@@ -123,7 +123,7 @@ PK_DEV uint32_t act_lds_offset(uint32_t k) { return k == 0 ? 0u : 4u * k + 12u; 
 // 16 distinct groups of 4 of the LDS's 64 four-byte banks; an even count
 // alone makes it a multiple of 8 dwords (16 blocks: a multiple of 64, every
 // row on the same banks).
-__host__ __device__ inline uint32_t act_row_pitch(uint32_t k_blocks) {
+__host__ __device__ constexpr uint32_t act_row_pitch(uint32_t k_blocks) {
     return k_blocks * kActLdsPitch + (k_blocks % 2u == 0u ? 16u : 0u);
 }
 
