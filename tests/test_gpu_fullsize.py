@@ -52,6 +52,14 @@ DENSE_FULL = [
     ("q6k_8192x4096_t2", QUANT_Q6_K, 8192, 4096, 2),
     ("q4k_8192x4096_t4", QUANT_Q4_K, 8192, 4096, 4),
     ("q4k_4096x4096_t64_prefill", QUANT_Q4_K, 4096, 4096, 64),
+    # K not a whole number of chunk groups: 32-row tiles with two 4-super-
+    # block chunks in flight (prefetches clamped past K, a tail chunk wholly
+    # past it, waves decoding a clamped copy that must add nothing), one and
+    # two token tiles; 16-row tiles with 8-super-block chunks
+    ("q6k_8192x2816_t16_ragged_k", QUANT_Q6_K, 8192, 2816, 16),
+    ("q4k_8192x3328_t12_ragged_k", QUANT_Q4_K, 8192, 3328, 12),
+    ("q6k_8192x2816_t31_ragged_k", QUANT_Q6_K, 8192, 2816, 31),
+    ("q6k_4096x2816_t9_ragged_k", QUANT_Q6_K, 4096, 2816, 9),
 ]
 
 
