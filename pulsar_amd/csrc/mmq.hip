@@ -702,12 +702,14 @@ PK_DEV float gather_pairs(const float (&f)[4]) {
                                         __float_as_uint(f[3])));
 }
 
-// Waves per block, 16 rows each. MXFP4 blocks take 8: their pair tiles are
-// large (16 pairs of 2880-value rows, ~58 KiB), and sharing one tile over
-// 128 rows keeps twice the waves per CU resident (c5 64-token layer 215 ->
-// 203 us); the K-quant layers measured slower with 8 (c4 Q2_K 183 -> 192 us).
+// Waves per block, 16 rows each. MXFP4 blocks take 12: their pair tiles are
+// large (16 pairs of 2880-value rows, ~58 KiB, one block per CU), and
+// sharing one tile over more rows keeps more waves per CU resident (c5
+// 64-token layer: 4 waves 215 us, 8 waves 196 us, 12 waves 185 us, 2880 rows
+// in 15 whole blocks; 16 waves, 128 VGPRs and 12 blocks per group, 221 us);
+// the K-quant layers measured slower with 8 (c4 Q2_K 183 -> 192 us).
 template <uint32_t Q>
-constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 8u : 4u;
+constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 12u : 4u;
 
 // amdgpu_waves_per_eu(2): register allocation for at least two waves per
 // SIMD. Left to itself the compiler spends more (Q2_K pair 164 VGPRs, Q4_K
