@@ -41,10 +41,17 @@ __global__ __launch_bounds__(256) void router_logits_q8_kernel(
     quantize_block_wave<4u, 260u>(x + (uint64_t)row * in_dim, in_dim, b, (uint8_t *)(xq + gblk));
 }
 
+// Waves per routed pair block (the first routes the token for all of them;
+// the staging of MXFP4 rows takes 2 NPL KiB of LDS per wave). Blocks of 8
+// waves, which route half as often per row, measured the same (c3 16.8 us,
+// c5 batch 1 35.2 us).
+template <uint32_t Q>
+constexpr uint32_t kRoutedWaves = 4u;
+
 // grid (row blocks, k_used + n_shared, n_tok); the pair stage of
 // moe_pair_kernel for the slot's expert, routed in-block.
 template <uint32_t Q, uint32_t UPLMAX, uint32_t J, uint32_t NPL, uint32_t RPW>
-__global__ __launch_bounds__(256) void moe_pair_routed_kernel(
+__global__ __launch_bounds__(64 * kRoutedWaves<Q>) void moe_pair_routed_kernel(
         float *__restrict__ mid, pulsar_expert_ptrs *__restrict__ ptrs_out, float *__restrict__ slot_w_out,
         int32_t *__restrict__ sel_out, float *__restrict__ w_out, const float *__restrict__ logits,
         const float *__restrict__ rbias, uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode,
@@ -79,7 +86,7 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
     }
     const pulsar_expert_ptrs &p = r.p;
     const uint32_t rpp = 64u >> lpr_log2;
-    const uint32_t pass0 = (blockIdx.x * 4u + threadIdx.x / 64u) * RPW;
+    const uint32_t pass0 = (blockIdx.x * kRoutedWaves<Q> + threadIdx.x / 64u) * RPW;
     if (!p.gate || !p.up) {  // unrouted slot contributes zero (pulsar_kernels.cu:2587-2590)
 #pragma unroll
         for (uint32_t k = 0; k < RPW; k++) {
@@ -88,7 +95,8 @@ __global__ __launch_bounds__(256) void moe_pair_routed_kernel(
         }
         return;
     }
-    pair_passes<Q, UPLMAX, NPL, RPW>(mid + so * mid_dim, p, r.w, a, rg, pass0, mid_dim, row_bytes, act_op, lut);
+    pair_passes<Q, UPLMAX, NPL, RPW, kRoutedWaves<Q>>(mid + so * mid_dim, p, r.w, a, rg, pass0, mid_dim, row_bytes,
+                                                      act_op, lut);
 }
 
 constexpr uint32_t kFusedMaxPass = 8;  // row passes per block in the fused down
@@ -264,10 +272,10 @@ struct PairRoutedLaunch {
     // launches) measured slower here, the routing being on every block's path
     template <uint32_t Q, uint32_t U, uint32_t J, uint32_t NPL>
     int go_j() {
-        const uint32_t rpb = 4u * (64u >> g.l2);
+        const uint32_t rpb = kRoutedWaves<Q> * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_slots, n_tok);
-        hipLaunchKernelGGL((moe_pair_routed_kernel<Q, U, J, NPL, 1>), grid, dim3(256), 0, pk::stream(), (float *)mid,
-                           (pulsar_expert_ptrs *)ptrs_out, (float *)slot_w_out, (int32_t *)sel_out,
+        hipLaunchKernelGGL((moe_pair_routed_kernel<Q, U, J, NPL, 1>), grid, dim3(64u * kRoutedWaves<Q>), 0, pk::stream(),
+                           (float *)mid, (pulsar_expert_ptrs *)ptrs_out, (float *)slot_w_out, (int32_t *)sel_out,
                            (float *)w_out, (const float *)logits, (const float *)rbias, n_expert, k_used, scale,
                            mode, bank, shared, (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2,
                            g.blocks, mid_dim, row_bytes, act_op);

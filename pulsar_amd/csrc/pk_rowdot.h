@@ -231,9 +231,9 @@ PK_DEV void load_one_row(const uint8_t *row, const RowGeom &rg, typename Fmt<Q>:
 // A wave's gate / up row pair, one pass ahead: issue() starts the loads
 // of the next pass (into registers: the units, or for NPL > 0 the aligned
 // pieces of the MXFP4 rows), land() makes them the current units wg / wu
-// (through the wave's 2 NPL KiB of LDS when staged). The loads of pass k+1
-// are in flight while pass k is computed.
-template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL>
+// (through the wave's 2 NPL KiB of LDS when staged; blocks of at most MAXW
+// waves). The loads of pass k+1 are in flight while pass k is computed.
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t MAXW = 4>
 struct PairRowPipe {
     typename Fmt<Q>::W wg[UPLMAX], wu[UPLMAX];
     typename Fmt<Q>::W ng[NPL ? 1 : UPLMAX], nu[NPL ? 1 : UPLMAX];
@@ -255,7 +255,7 @@ struct PairRowPipe {
                 wu[i] = nu[i];
             }
         } else {
-            __shared__ __align__(16) uint8_t stage[4][2][NPL * 1024u];
+            __shared__ __align__(16) uint8_t stage[MAXW][2][NPL * 1024u];
             uint8_t(&mine)[2][NPL * 1024u] = stage[threadIdx.x / 64u];
             const uint8_t *lg = sg.store(mine[0]);
             const uint8_t *lu = su.store(mine[1]);
@@ -270,13 +270,13 @@ struct PairRowPipe {
 // The pair stage of RPW consecutive row passes of one (token, slot):
 // mid_row[row] = glu(gate . x + gate_b, up . x + up_b) * w for the wave's
 // rows (pulsar_kernels.cu:2606-2612: bias on the projection output, then
-// the combine, then the router weight).
-template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t RPW>
+// the combine, then the router weight). Blocks of at most MAXW waves.
+template <uint32_t Q, uint32_t UPLMAX, uint32_t NPL, uint32_t RPW, uint32_t MAXW = 4>
 PK_DEV void pair_passes(float *mid_row, const pulsar_expert_ptrs &p, float w, const Act (&a)[UPLMAX],
                         const RowGeom &rg, uint32_t pass0, uint32_t mid_dim, uint64_t row_bytes, uint32_t act_op,
                         const uint2 *lut) {
     const uint32_t rpp = 64u >> rg.lpr_log2;
-    PairRowPipe<Q, UPLMAX, NPL> pipe;
+    PairRowPipe<Q, UPLMAX, NPL, MAXW> pipe;
     auto off = [&](uint32_t k) {
         const uint32_t row = (pass0 + k) * rpp + rg.rip;
         return (uint64_t)(row < mid_dim ? row : 0u) * row_bytes;
