@@ -548,7 +548,7 @@ def pmc_run(ctx, which: str):
             copies = dev_copies(torch, w, 1_000_000_000)
             rb = fm.row_bytes(q, cols)
             alg = {}
-            for n_tok, kern in ((1, "pk::matvec_kernel<4u, 1u, 1u, 1u, 6u>"), (16, "pk::mmq_gemm_kernel<4u, 2u, 4u, 1u>")):
+            for n_tok, kern in ((1, "pk::matvec_kernel<4u, 1u, 1u, 1u, 6u>"), (16, "pk::mmq_gemm_kernel<4u, 2u, 4u, 1u, 2u>")):
                 x = torch.from_numpy(synth.activations(n_tok, cols, synth.rng_for(12, "pmc"))).cuda()
                 xq = torch.zeros(n_tok * fm.q8k_blocks(cols) * 292, dtype=torch.uint8, device="cuda")
                 K.quantize_q8_k(xq, x, cols, n_tok)
