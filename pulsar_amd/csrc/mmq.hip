@@ -519,11 +519,18 @@ static int launch_gemm_q(float *out, const uint8_t *w, const pulsar_block_q8_K *
     // below 8192 rows a 32-row tile leaves CUs idle (4096 rows: 128 blocks);
     // 16-row tiles with 8 super-blocks per chunk measured fastest there
     // (Q4_K 4096 x 4096, 16 tokens: 8.7 -> 6.9 us), 32-row tiles with 4
-    // above (Q6_K 8192 x 4096: 11.8 us; 16-row tiles 12.9-14.0 us)
+    // above (Q6_K 8192 x 4096: 11.8 us; 16-row tiles 12.9-14.0 us). Q4_K
+    // takes 32-row tiles with 8 super-blocks per chunk above: 16 waves per
+    // block, 4 per SIMD within 128 VGPRs (cold weights, 16 tokens: 8192 x
+    // 4096 11.1 -> 9.9 us, 14336 x 4096 19.2 -> 16.6 us; 5-31 tokens and
+    // 14336-wide rows alike); Q6_K and NVFP4 spill at that cap (Q6_K 8192 x
+    // 4096 12.8 -> 21.5 us)
     if (n_tok >= PK_GEMM_NT2)
         PK_GEMM(2, 2, 2, PK_GEMM_D_NT2);
     else if (out_dim < 8192u)
         PK_GEMM(1, 8, 1, PK_GEMM_D_R16);
+    else if (Q == PULSAR_QUANT_Q4_K)
+        PK_GEMM(2, 8, 1, 1);
     else
         PK_GEMM(2, 4, 1, PK_GEMM_D_R32);
 #undef PK_GEMM

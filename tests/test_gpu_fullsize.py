@@ -60,6 +60,9 @@ DENSE_FULL = [
     ("q4k_8192x3328_t12_ragged_k", QUANT_Q4_K, 8192, 3328, 12),
     ("q6k_8192x2816_t31_ragged_k", QUANT_Q6_K, 8192, 2816, 31),
     ("q6k_4096x2816_t9_ragged_k", QUANT_Q6_K, 4096, 2816, 9),
+    # Q4_K at 8192 rows and more: 32-row tiles, 8-super-block chunks, 16 waves
+    ("q4k_8192x4096_t16", QUANT_Q4_K, 8192, 4096, 16),
+    ("q4k_14336x4096_t31", QUANT_Q4_K, 14336, 4096, 31),
 ]
 
 
