@@ -5,8 +5,8 @@
 //     super-blocks and the partials are added in wave order through LDS
 //     (deterministic);
 //   moe_grouped_mmq_kq_kernel: the grouped MoE stages (16 rows x up to 16
-//     (token, slot) pairs of one expert per MFMA tile) for Q2_K, IQ2_XXS and
-//     MXFP4 experts.
+//     (token, slot) pairs of one expert per MFMA tile) for Q2_K, IQ2_XXS,
+//     MXFP4, Q4_K, Q5_K and Q6_K experts.
 // Every kernel produces exact int32 group sums with MFMA, applies the
 // format's integer scales in int32, forms the per-super-block fp32 value in
 // the reference's operation order and accumulates super-blocks in order.
@@ -554,8 +554,8 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
 }
 
 // ------------------------------------ grouped Q2_K / IQ2_XXS / MXFP4 (MoE) --
-// Block = 64 rows (16 per wave) x up to kGqPairs pairs of one expert group,
-// the whole K per wave (no split). The pairs' q8_K rows are staged in LDS
+// Block = 16 rows per wave (kGqWaves waves: 64 rows, MXFP4 192) x up to
+// kGqPairs pairs of one expert group, the whole K per wave (no split). The pairs' q8_K rows are staged in LDS
 // once per pair tile (load_act_lds layout); each wave streams its 16 rows
 // super-block by super-block: a contiguous copy (consecutive lanes on
 // consecutive bytes of a row) to registers, the next super-block's copy in
