@@ -6,14 +6,14 @@
 
 namespace pk {
 
-// sigmoid as pulsar_kernels.cu:913-921
+// sigmoid as pulsar_kernels.cu:913-921: x >= 0 gives 1 / (1 + exp(-x)),
+// otherwise exp(x) / (1 + exp(x)). Both sides take exp(-|x|) (the same
+// argument, -0 included), so one exp and one division with the numerator
+// selected give the same bits without a divergent branch that would run
+// both sides (NaN: exp(NaN) / (1 + NaN) = NaN either way).
 PK_DEV float router_sigmoid(float x) {
-    if (x >= 0.0f) {
-        const float e = expf(-x);
-        return 1.0f / (1.0f + e);
-    }
-    const float e = expf(x);
-    return e / (1.0f + e);
+    const float e = expf(-fabsf(x));
+    return (x >= 0.0f ? 1.0f : e) / (1.0f + e);
 }
 
 constexpr uint32_t kMaxPerLane = 16;  // 64 lanes x 16 = 1024 routed logits
