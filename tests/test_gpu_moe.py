@@ -308,6 +308,38 @@ def test_router_select_ties_inf_nan(dev, mode):
     assert np.allclose(got_w[ok], want_w[ok], rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_router_select_sigmoid_edges(dev, with_bias):
+    """Sigmoid scores (mode 0) at the edges of both of its branches: +-0,
+    +-inf, NaN, logits that saturate the sigmoid to exactly 1 (ties broken
+    by the lower index) and large negative logits whose scores are tiny
+    but well separated."""
+    n_expert, k, n_tok = 256, 8, 4
+    logits = (rng.standard_normal((n_tok, n_expert)) * 3).astype(np.float32)
+    logits[0, ::5] = 40.0                                   # sigmoid == 1: a tie run
+    logits[0, 1] = -0.0
+    logits[0, 2] = 0.0
+    logits[1, :] = -np.inf
+    logits[1, 20:40] = -(30.0 + np.arange(20, dtype=np.float32))  # exp(x) / (1 + exp(x)) branch
+    logits[1, 50] = np.nan
+    logits[2, :] = np.nan
+    logits[2, 7] = np.inf
+    logits[2, 9] = -np.inf
+    logits[3, ::2] = -0.0
+    logits[3, 1::2] = 0.0
+    bias = ((rng.standard_normal(n_expert) * 0.25).astype(np.float32) if with_bias
+            else np.zeros(n_expert, np.float32))
+    sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
+    w = zeros_f32((n_tok, k))
+    K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.0, n_tok, 0, 0)
+    want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.0, n_tok, 0, 0)
+    assert np.array_equal(down(sel), want_sel)
+    got_w = down(w)
+    assert np.array_equal(np.isnan(got_w), np.isnan(want_w))
+    ok = ~np.isnan(want_w)
+    assert np.allclose(got_w[ok], want_w[ok], rtol=0, atol=1e-6)
+
+
 def test_matmul_f32_and_bias(dev):
     for in_dim, out_dim, n_tok in ((2048, 256, 1), (4096, 128, 16), (2880, 32, 64), (37, 5, 3)):
         wt = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float32)
