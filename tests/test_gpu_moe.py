@@ -251,6 +251,62 @@ def test_grouped_mxfp4_mfma(dev, n_tok):
     assert (err <= down_bound(L, midq)).all(), f"grouped mfma down: max err {err.max():.3e}"
 
 
+def _random_grouped_cases(n_per_format=3):
+    """Seeded random grouped-layer shapes per format: input widths with odd
+    and even super-block counts (the staged pair rows' pitch differs), row
+    counts off the block size, 1-11 tokens of 1-4 slots over 2-9 experts
+    (a slot may repeat its token's expert), NULL slots."""
+    r = np.random.default_rng(8191)
+    cases = []
+    for q in (QUANT_Q2_K, QUANT_IQ2_XXS, QUANT_Q4_K, fm.QUANT_Q5_K, QUANT_Q6_K, QUANT_MXFP4):
+        for _ in range(n_per_format):
+            if q == QUANT_MXFP4:
+                hidden, ffn = 32 * int(r.integers(8, 48)), 32 * int(r.integers(4, 16))
+            else:
+                hidden, ffn = 256 * int(r.integers(1, 7)), 256 * int(r.integers(1, 3))
+            E, n_used, n_tok = int(r.integers(2, 10)), int(r.integers(1, 5)), int(r.integers(1, 12))
+            n_null = int(r.integers(0, 3))
+            nulls = tuple(int(v) for v in r.choice(n_tok * n_used, size=min(n_null, n_tok * n_used - 1),
+                                                    replace=False)) if n_tok * n_used > 1 else ()
+            cases.append((q, hidden, ffn, E, n_used, n_tok, nulls, int(r.integers(0, 1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("q,hidden,ffn,E,n_used,n_tok,nulls,seed", _random_grouped_cases())
+def test_grouped_random_shapes(dev, q, hidden, ffn, E, n_used, n_tok, nulls, seed):
+    """Grouped pair and down stages against the oracle on seeded random
+    shapes (every grouped format; MXFP4 with biases and swiglu_oai)."""
+    mx = q == QUANT_MXFP4
+    act = ACT_SWIGLU_OAI if mx else ACT_SILU
+    L = Layer(q, q, hidden=hidden, ffn=ffn, E=E, n_used=n_used, n_tok=n_tok, biases=mx, null_slots=nulls,
+              seed=seed)
+    hptrs, dptrs = L.ptrs()
+    xq = oracle.quantize_q8_k(L.x)
+    want_mid = oracle.moe_pair_swiglu(hptrs, L.w, xq, L.hidden, L.ffn, L.n_used, L.n_tok, L.grb, L.gq, act)
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    mid = zeros_f32((L.n_tok * L.n_used, L.ffn))
+    K.moe_pair_swiglu_grouped(mid, gptrs, up(starts), up(pairs), up_f32(L.w), up(xq), L.hidden, L.ffn,
+                              L.n_used, len(ids), L.grb, q, act)
+    got_mid = down(mid)
+    bound = pair_bound(L, xq, act) + 4e-7 * np.abs(want_mid) + 1e-30
+    err = np.abs(got_mid.astype(np.float64) - want_mid)
+    assert (err <= bound).all(), f"grouped pair: max err {err.max():.3e} (worst ratio {(err / bound).max():.2f})"
+    for si, e in enumerate(L.sel.reshape(-1)):
+        if e < 0:
+            assert not got_mid[si].any()
+    midq = oracle.quantize_q8_k(want_mid)
+    partial = zeros_f32((L.n_tok * L.n_used, L.hidden))
+    K.moe_down_grouped(partial, gptrs, up(starts), up(pairs), up(midq), L.ffn, L.hidden, L.n_used, len(ids),
+                       L.drb, q)
+    out = zeros_f32((L.n_tok, L.hidden))
+    K.moe_slot_sum(out, partial, L.hidden, L.n_used, L.n_tok)
+    want = oracle.moe_down(hptrs, midq, L.ffn, L.hidden, L.n_used, L.n_tok, L.drb, q)
+    err = np.abs(down(out).astype(np.float64) - want)
+    bound = down_bound(L, midq)
+    assert (err <= bound).all(), f"grouped down: max err {err.max():.3e} (worst ratio {(err / bound).max():.2f})"
+
+
 def test_grouped_contract(dev):
     buf = up(np.zeros(4096, np.uint8))
     with pytest.raises(K.KernelError):  # in_dim % 256 (pulsar_kernels.cu:3488)
