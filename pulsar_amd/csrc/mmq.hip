@@ -588,22 +588,33 @@ struct GmmqFmt;
 // kTails small loads (tail_off, kTailBytes each) to kTailSlot + c. `lim`
 // bounds the clamped unit (super-blocks, or 32-blocks for MXFP4; kLimPerSb
 // of them per super-block); consecutive super-blocks are kSbBytes apart.
+// Q2_K and Q6_K copy their f16 scales as one more 16-byte piece that starts
+// at them (slot kTailSlot): a separate 2- or 4-byte load per (row, super-
+// block) touches a new cache line in every lane. The piece of a row's last
+// super-block is held inside the row, which puts the scales kTailLast bytes
+// further into it. Measured: c4 Q2_K gate / up weight stream alone 86 ->
+// 74 us (the stage ~99 -> ~97 us, now held by its decode), Q6_K down stages
+// of 16- and 64-token Q4_K / Q6_K layers 3-6% faster. IQ2_XXS keeps its
+// separate d load: a d piece (2-byte aligned, overlapping the first code
+// piece) made its gate / up stage slower (110 -> 123 us).
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q2_K> {
-    static constexpr uint32_t kPieces = 5, kTails = 1, kTailBytes = 4;
+    static constexpr uint32_t kPieces = 6, kTails = 0, kTailBytes = 4;
     static constexpr uint32_t kSbBytes = 84, kLimPerSb = 1;
-    static constexpr uint32_t kTailSlot = 80;  // d, dmin
-    static constexpr uint32_t kSlot = 96;      // LDS bytes per row super-block
+    static constexpr uint32_t kTailSlot = 80, kTailLast = 12;  // d, dmin
+    static constexpr uint32_t kSlot = 96;                      // LDS bytes per row super-block
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
-        return (sb < lim ? sb : lim - 1u) * 84u + 16u * c;  // scales, qs: bytes 0..79
+        // scales, qs: bytes 0..79; piece 5 from d, dmin
+        const uint32_t o = (sb < lim ? sb : lim - 1u) * 84u + 16u * c;
+        return o < 84u * lim - 16u ? o : 84u * lim - 16u;
     }
-    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t, uint32_t lim) { return (sb < lim ? sb : lim - 1u) * 84u + 80u; }
+    PK_DEV static uint32_t tail_off(uint32_t, uint32_t, uint32_t) { return 0u; }
 };
 template <>
 struct GmmqFmt<PULSAR_QUANT_IQ2_XXS> {
     static constexpr uint32_t kPieces = 4, kTails = 1, kTailBytes = 4;
     static constexpr uint32_t kSbBytes = 66, kLimPerSb = 1;
-    static constexpr uint32_t kTailSlot = 64;  // d (the upper 2 bytes unused)
+    static constexpr uint32_t kTailSlot = 64, kTailLast = 0;  // d (the upper 2 bytes unused)
     static constexpr uint32_t kSlot = 80;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
         return (sb < lim ? sb : lim - 1u) * 66u + 2u + 16u * c;  // the 8 groups: bytes 2..65
@@ -616,7 +627,7 @@ struct GmmqFmt<PULSAR_QUANT_MXFP4> {
     // to slot 128 + c
     static constexpr uint32_t kPieces = 8, kTails = 8, kTailBytes = 1;
     static constexpr uint32_t kSbBytes = 136, kLimPerSb = 8;  // lim counts 32-blocks
-    static constexpr uint32_t kTailSlot = 128;
+    static constexpr uint32_t kTailSlot = 128, kTailLast = 0;
     static constexpr uint32_t kSlot = 144;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
         const uint32_t b = 8u * sb + c;
@@ -631,7 +642,7 @@ template <>
 struct GmmqFmt<PULSAR_QUANT_Q4_K> {
     static constexpr uint32_t kPieces = 9, kTails = 0, kTailBytes = 4;  // the whole 144 bytes
     static constexpr uint32_t kSbBytes = 144, kLimPerSb = 1;
-    static constexpr uint32_t kTailSlot = 0;
+    static constexpr uint32_t kTailSlot = 0, kTailLast = 0;
     static constexpr uint32_t kSlot = 144;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
         return (sb < lim ? sb : lim - 1u) * 144u + 16u * c;
@@ -642,7 +653,7 @@ template <>
 struct GmmqFmt<PULSAR_QUANT_Q5_K> {
     static constexpr uint32_t kPieces = 11, kTails = 0, kTailBytes = 4;  // the whole 176 bytes
     static constexpr uint32_t kSbBytes = 176, kLimPerSb = 1;
-    static constexpr uint32_t kTailSlot = 0;
+    static constexpr uint32_t kTailSlot = 0, kTailLast = 0;
     static constexpr uint32_t kSlot = 176;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
         return (sb < lim ? sb : lim - 1u) * 176u + 16u * c;
@@ -651,14 +662,15 @@ struct GmmqFmt<PULSAR_QUANT_Q5_K> {
 };
 template <>
 struct GmmqFmt<PULSAR_QUANT_Q6_K> {
-    static constexpr uint32_t kPieces = 13, kTails = 1, kTailBytes = 2;  // bytes 0..207, then d
+    static constexpr uint32_t kPieces = 14, kTails = 0, kTailBytes = 2;  // bytes 0..207, piece 13 from d
     static constexpr uint32_t kSbBytes = 210, kLimPerSb = 1;
-    static constexpr uint32_t kTailSlot = 208;
+    static constexpr uint32_t kTailSlot = 208, kTailLast = 14;
     static constexpr uint32_t kSlot = 224;
     PK_DEV static uint32_t piece_off(uint32_t sb, uint32_t c, uint32_t lim) {
-        return (sb < lim ? sb : lim - 1u) * 210u + 16u * c;
+        const uint32_t o = (sb < lim ? sb : lim - 1u) * 210u + 16u * c;
+        return o < 210u * lim - 16u ? o : 210u * lim - 16u;
     }
-    PK_DEV static uint32_t tail_off(uint32_t sb, uint32_t, uint32_t lim) { return (sb < lim ? sb : lim - 1u) * 210u + 208u; }
+    PK_DEV static uint32_t tail_off(uint32_t, uint32_t, uint32_t) { return 0u; }
 };
 #ifndef PK_GQ_SBS
 #define PK_GQ_SBS 2u
@@ -841,6 +853,9 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         }
         // super-block sb from the wave's LDS slot ws (row i of matrix 0)
         auto sb_compute = [&](uint32_t sb, const uint8_t *ws) {
+            // the scales' slot offset (the row's last super-block: its copy is
+            // held inside the row)
+            const uint32_t tail_at = F::kTailSlot + (sb + 1u == lim ? F::kTailLast : 0u);
             const uint8_t *rec = ar + sb * kActLdsPitch;  // d @0, q8 values @16, bsums @272
             // pairs past the tile read the last pair's values: their MFMA
             // rows and sums are never stored
@@ -899,7 +914,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 int32_t isum[NM][4];
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    wv[mt] = MmaQ6K::load_lds(ws + mt * 16u * kRowL, kq, F::kTailSlot);
+                    wv[mt] = MmaQ6K::load_lds(ws + mt * 16u * kRowL, kq, tail_at);
 #pragma unroll
                     for (int r = 0; r < 4; r++) isum[mt][r] = 0;
                 }
@@ -1025,7 +1040,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                     const uint2 zero = make_uint2(0u, 0u);
                     const v4i dl = mfma16x16x32(alh, kq < 2u ? mn : zero);
                     const v4i dh = mfma16x16x32(alh, kq < 2u ? zero : mn);
-                    const uint32_t dd = *(const uint32_t *)(ws + mt * 16u * kRowL + F::kTailSlot);
+                    const uint32_t dd = *(const uint32_t *)(ws + mt * 16u * kRowL + tail_at);
                     const float xd = f16f((uint16_t)dd), xmin = f16f((uint16_t)(dd >> 16));
                     if (small) {
                         const v4i sm = {dl[0] + 128 * dh[0], dl[1] + 128 * dh[1], dl[2] + 128 * dh[2], dl[3] + 128 * dh[3]};
