@@ -593,8 +593,9 @@ struct GmmqFmt;
 // block) touches a new cache line in every lane. The piece of a row's last
 // super-block is held inside the row, which puts the scales kTailLast bytes
 // further into it. Measured: c4 Q2_K gate / up weight stream alone 86 ->
-// 74 us (the stage ~99 -> ~97 us, now held by its decode), Q6_K down stages
-// of 16- and 64-token Q4_K / Q6_K layers 3-6% faster. IQ2_XXS keeps its
+// 74 us (with the decode the stage 99.6 -> 98.1 us, the layer 164.9 ->
+// 161.5 us), Q6_K down stages of 16- and 64-token Q4_K / Q6_K layers 3-6%
+// faster. IQ2_XXS keeps its
 // separate d load: a d piece (2-byte aligned, overlapping the first code
 // piece) made its gate / up stage slower (110 -> 123 us).
 template <>
