@@ -26,9 +26,10 @@ result configurations covers at least 2.2 GB of weights whatever --steps is
 (it times max(K, enough steps) and reports the time per step), so the 256 MB
 Infinity Cache cannot serve them; each layer step routes a different seeded
 token batch. Timing: HIP events on the per-thread default stream (the stream
-every pulsar_* launch uses) around the steps, eagerly and as one HIP-graph
-replay captured on that stream (the reference decodes from CUDA graphs,
-crates/kernels/src/lib.rs:755-811); the graph figure is the reported one.
+every pulsar_* launch uses) around the steps, eagerly and as HIP-graph
+replays captured on that stream (the reference decodes from CUDA graphs,
+crates/kernels/src/lib.rs:755-811); the reported figure is the median of
+five timed replays, each of the same K steps between synchronizations.
 
 cpu_baseline: the oracle's C restatement of the reference CPU lane
 (oracle/pulsar_oracle.c, AVX2 dots bit-identical to the scalar ones, the
@@ -79,9 +80,13 @@ def parse_args():
 class Timer:
     """HIP events on the launch stream (the per-thread default stream every
     pulsar_* launch uses) around n steps, two ways: eager launches from
-    Python, and one replay of a HIP graph holding the same n steps, captured
+    Python, and replays of a HIP graph holding the same n steps, captured
     on that stream as the reference's decode graphs are
-    (crates/kernels/src/lib.rs:755-811)."""
+    (crates/kernels/src/lib.rs:755-811). The graph figure is the median of
+    REPLAYS timed replays, each of exactly n steps between synchronizations
+    (one replay of a ~3 ms layer chain moved by up to 5% from run to run)."""
+
+    REPLAYS = 5
 
     def __init__(self, torch, K):
         from pulsar_amd import runtime
@@ -103,14 +108,16 @@ class Timer:
         g = rt.Graph.capture(lambda: [step(warmup + i) for i in range(steps)])
         g.launch()  # warm replay
         rt.sync()
-        e0.record()
-        g.launch()
-        e1.record()
-        e1.synchronize()
-        graph = e0.elapsed_ms(e1) / steps
+        times = []
+        for _ in range(self.REPLAYS):
+            e0.record()
+            g.launch()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_ms(e1) / steps)
         del g
         rt.sync()
-        return {"ms": graph, "ms_eager": eager}
+        return {"ms": float(np.median(times)), "ms_eager": eager, "ms_replays": [round(t, 6) for t in times]}
 
 
 def dev_copies(torch, host: np.ndarray, min_total: int, slack: int = 256):
@@ -349,6 +356,7 @@ def bench_moe(ctx, spec, steps, warmup, path: str, exact_steps: bool = False, st
         "GBps": alg / (ms * 1e-3) / 1e9,
         "layer_banks": n_banks,
         "layers_per_replay": n,
+        "us_per_layer_replays": [round(t * 1e3, 3) for t in tm["ms_replays"]],
     }
     res["pct_of_peak"] = 100 * res["GBps"] / HBM_PEAK_GBS
     if stage_timing:
