@@ -57,6 +57,7 @@ def load() -> ctypes.CDLL:
         "po_set_simd": (_int, [_int]),
         "po_rows_dot": (_int, [_vp, _vp, _u64, _u32, _vp, _u32, _u32, _u32, _u32, _vp]),
         "po_avx2_supported": (_int, []),
+        "po_avx2_vec_dot": (_f32, [_u32, _vp, _vp, _u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -115,11 +116,17 @@ def block_dot(quant: int, row: np.ndarray, b: int, yblock: np.ndarray, n_valid32
     return f, i0.value, i1.value, sumi
 
 
-def vec_dot(quant: int, row: np.ndarray, xq: np.ndarray, n: int):
-    """(row dot, sum_b |f_b|) of one row against one q8_K row."""
-    a = ctypes.c_double()
+def vec_dot(quant: int, row: np.ndarray, xq: np.ndarray, n: int, abs_sum: bool = True):
+    """(row dot, sum_b |f_b|) of one row against one q8_K row.
+
+    With abs_sum=False no magnitude sum is requested (None is returned for
+    it), which lets po_vec_dot take its AVX2 row dots where they exist; with
+    a magnitude sum it always walks the scalar per-block dots."""
     row = np.ascontiguousarray(row, dtype=np.uint8)
     xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    if not abs_sum:
+        return load().po_vec_dot(quant, _p(row), _p(xq), n, None), None
+    a = ctypes.c_double()
     f = load().po_vec_dot(quant, _p(row), _p(xq), n, ctypes.addressof(a))
     return f, a.value
 
@@ -168,6 +175,14 @@ def set_simd(on: bool) -> bool:
 
 def avx2_supported() -> bool:
     return bool(load().po_avx2_supported())
+
+
+def avx2_vec_dot(quant: int, row: np.ndarray, xq: np.ndarray, n: int) -> float:
+    """The AVX2 row dot itself (oracle/lane_avx2.c), whatever the SIMD
+    setting; Q4_K / Q2_K / IQ2_XXS, n a multiple of 256, AVX2 hosts only."""
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    return load().po_avx2_vec_dot(quant, _p(row), _p(xq), n)
 
 
 def glu(g: float, u: float, op: int) -> float:

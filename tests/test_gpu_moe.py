@@ -339,6 +339,23 @@ def test_router_select(dev, n_expert, k, n_tok, mode):
     assert np.allclose(down(w), want_w, rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("n_expert,k,n_tok", [(256, 8, 1), (128, 8, 16), (32, 4, 64)])
+def test_router_select_softmax_with_selection_bias(dev, n_expert, k, n_tok):
+    """Mode 1 selects on raw logit + bias and weights the winners by their
+    raw logits (pulsar_kernels.cu:968-971, 1036-1046); the biases are large
+    enough to change the selection."""
+    logits = (rng.standard_normal((n_tok, n_expert)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(n_expert) * 2).astype(np.float32)
+    sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
+    w = zeros_f32((n_tok, k))
+    K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.5, n_tok, 1, 0)
+    want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.5, n_tok, 1, 0)
+    raw_sel, _ = oracle.router_select(logits, np.zeros(n_expert, np.float32), n_expert, k, 1.5, n_tok, 1, 0)
+    assert not np.array_equal(want_sel, raw_sel)
+    assert np.array_equal(down(sel), want_sel)
+    assert np.allclose(down(w), want_w, rtol=0, atol=1e-6)
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 def test_router_select_ties_inf_nan(dev, mode):
     """Tied scores go to the lower index; -inf and NaN logits: NaN never

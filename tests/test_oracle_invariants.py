@@ -238,6 +238,105 @@ def test_router_softmax_mode_equals_llama_order():
             assert np.allclose(w[t], p[top] / p[top].sum(), atol=1e-5, rtol=0)
 
 
+def _f32_ulps(a, b):
+    """Distance in f32 units in the last place (finite values)."""
+    ia = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, np.int64(-(2 ** 31)) - ia, ia)
+    ib = np.where(ib < 0, np.int64(-(2 ** 31)) - ib, ib)
+    return np.abs(ia - ib)
+
+
+def _matmul_f32_closed(w, x):
+    """out[t][o] = sum_i w[o][i] x[t][i] (pulsar_kernels.cu:6504-6535) in
+    f64 by numpy's own product, rounded once to f32."""
+    return (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+
+
+@pytest.mark.parametrize("out_dim,in_dim,n_tok", [(256, 2048, 3), (128, 4096, 2), (32, 2880, 4), (7, 300, 1)])
+def test_matmul_f32_equals_f64_closed_form(out_dim, in_dim, n_tok):
+    """po_matmul_f32 against an f64 product by another route (numpy's
+    blocked matmul), rounded to f32: within 1 ulp (the two f64 sums differ
+    only in order, so the f32 roundings can differ at a rounding boundary)."""
+    w = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float32)
+    x = rng.standard_normal((n_tok, in_dim)).astype(np.float32)
+    got = oracle.matmul_f32(w, x, in_dim, out_dim, n_tok)
+    want = _matmul_f32_closed(w, x)
+    assert _f32_ulps(got, want).max() <= 1
+    # an f32 running sum (a plausible mistake) is further than 1 ulp away
+    acc = np.zeros((n_tok, out_dim), np.float32)
+    for i in range(in_dim):
+        acc += x[:, i:i + 1] * w[None, :, i]
+    if in_dim >= 2048:
+        assert _f32_ulps(acc, want).max() > 1
+
+
+def test_matmul_f32_closed_form_catches_transpose_and_token_swap():
+    """The comparison above fails for a transposed weight operand and for
+    swapped tokens, so it pins the operand roles and the output layout."""
+    n = 256
+    w = rng.standard_normal((n, n)).astype(np.float32)
+    x = rng.standard_normal((2, n)).astype(np.float32)
+    got = oracle.matmul_f32(w, x, n, n, 2)
+    assert _f32_ulps(got, _matmul_f32_closed(w, x)).max() <= 1
+    assert _f32_ulps(got, _matmul_f32_closed(np.ascontiguousarray(w.T), x)).max() > 1000
+    assert _f32_ulps(got, _matmul_f32_closed(w, x[::-1].copy())).max() > 1000
+
+
+def test_add_bias_rows_equals_broadcast_add():
+    """po_add_bias_rows (pulsar_kernels.cu:3621-3638) is x[r][i] + b[i] in
+    f32, bit for bit, and not b[r] or a bias of the wrong length."""
+    for rows, dim in ((1, 32), (4, 256), (64, 2880), (3, 7)):
+        x = rng.standard_normal((rows, dim)).astype(np.float32)
+        b = (rng.standard_normal(dim) * 0.02).astype(np.float32)
+        got = oracle.add_bias_rows(x, b, dim, rows)
+        assert np.array_equal(got.view(np.uint32), (x + b[None, :]).view(np.uint32))
+        if rows > 1 and dim > 1:
+            assert not np.array_equal(got, x + np.resize(b, rows)[:, None])
+
+
+def _mode1_closed(raw, bias, k, scale):
+    """Router mode 1 with a selection bias (pulsar_kernels.cu:968-971,
+    1036-1046): ids = top-k of f32(raw + bias), higher first, ties to the
+    lower index; weights = exp(raw_w - max raw_w) / sum * scale over the
+    winners' RAW logits, in f64."""
+    score = (raw + bias).astype(np.float32)
+    ids = sorted(range(len(raw)), key=lambda e: (-float(score[e]), e))[:k]
+    z = raw[ids].astype(np.float64)
+    p = np.exp(z - z.max())
+    return ids, p / p.sum() * scale
+
+
+@pytest.mark.parametrize("n_expert,k,seed", [(256, 8, 0), (128, 8, 1), (32, 4, 2), (9, 9, 3)])
+def test_router_softmax_mode_with_selection_bias(n_expert, k, seed):
+    r = np.random.default_rng(seed)
+    n_tok = 5
+    raw = (r.permutation(n_expert)[None, :] * 0.05 + r.integers(-3, 4, (n_tok, 1))).astype(np.float32)
+    raw[1] = raw[1][::-1]
+    # biases large enough to reorder the raw logits, so selection by raw
+    # alone and selection by raw + bias differ
+    bias = (r.permutation(n_expert) * 0.03 - n_expert * 0.015).astype(np.float32)
+    # an exact tie of raw + bias between two experts: the lower index wins
+    raw[2, 7 % n_expert] = raw[2, 3]
+    bias[7 % n_expert] = bias[3]
+    sel, w = oracle.router_select(raw, bias, n_expert, k, 2.5, n_tok, 1)
+    for t in range(n_tok):
+        ids, want = _mode1_closed(raw[t], bias, k, 2.5)
+        assert list(sel[t]) == ids, t
+        np.testing.assert_allclose(w[t].astype(np.float64), want, rtol=2e-6, atol=1e-7)
+    if k < n_expert:
+        # the bias changes the selection here, and weighting by raw + bias
+        # instead of raw (a plausible misreading) changes the weights
+        by_raw = [sorted(range(n_expert), key=lambda e: (-float(raw[t, e]), e))[:k] for t in range(n_tok)]
+        assert any(list(sel[t]) != by_raw[t] for t in range(n_tok))
+        ids, want = _mode1_closed(raw[0], bias, k, 2.5)
+        z = (raw[0, ids] + bias[ids]).astype(np.float64)
+        wrong = np.exp(z - z.max())
+        wrong = wrong / wrong.sum() * 2.5
+        assert np.abs(wrong - want).max() > 1e-3
+        assert np.abs(w[0] - wrong).max() > 1e-3
+
+
 def test_router_sigmoid_mode_and_ties():
     n_expert, k = 64, 8
     logits = (rng.standard_normal((3, n_expert)) * 4).astype(np.float32)

@@ -43,26 +43,38 @@ def _rows_and_acts(quant, rows, n, seed):
 @pytest.mark.parametrize("quant", LANE_FORMATS)
 @pytest.mark.parametrize("n,seed", [(256, 42), (2048, 99), (5120, 7331), (4096, 424242)])
 def test_avx2_dots_equal_scalar_bits(quant, n, seed):
+    """Three routes to each row dot: po_vec_dot with SIMD off (scalar
+    per-block dots), po_vec_dot with SIMD on and no magnitude sum requested
+    (the dispatch to the AVX2 dots), and the AVX2 dot called directly. All
+    three must agree bit for bit, including the activation row whose quants
+    reach +-127."""
     w, xq = _rows_and_acts(quant, 24, n, seed)
+    assert np.abs(oracle.q8k_fields(xq[2])[1].astype(int)).max() == 127
+
+    def dots(fn):
+        return np.array([[fn(w[r], xq[t]) for r in range(w.shape[0])] for t in range(xq.shape[0])], np.float32)
+
     got = {}
     for simd in (False, True):
         prev = oracle.set_simd(simd)
         try:
-            got[simd] = np.array([[oracle.vec_dot(quant, w[r], xq[t], n)[0] for r in range(w.shape[0])]
-                                  for t in range(xq.shape[0])], np.float32)
+            got[simd] = dots(lambda row, x: oracle.vec_dot(quant, row, x, n, abs_sum=False)[0])
         finally:
             oracle.set_simd(prev)
+    direct = dots(lambda row, x: oracle.avx2_vec_dot(quant, row, x, n))
     assert np.abs(got[False]).max() > 0
     assert np.array_equal(got[False].view(np.uint32), got[True].view(np.uint32))
+    assert np.array_equal(got[False].view(np.uint32), direct.view(np.uint32))
 
 
 @needs_avx2
 @pytest.mark.parametrize("quant", LANE_FORMATS)
 def test_avx2_threaded_lane_equals_scalar_lane(quant):
-    """The threaded matvec with AVX2 dots equals the serial scalar one."""
-    rows, n, n_tok = 600, 1024, 2
+    """The threaded matvec with AVX2 dots equals the serial scalar one, on
+    all three activation rows (the third reaches +-127)."""
+    rows, n = 600, 1024
     w, xq = _rows_and_acts(quant, rows, n, 555)
-    xq = np.ascontiguousarray(xq[:n_tok])
+    n_tok = xq.shape[0]
     rb = row_bytes(quant, n)
     prev = oracle.set_simd(False)
     try:
@@ -70,8 +82,10 @@ def test_avx2_threaded_lane_equals_scalar_lane(quant):
     finally:
         oracle.set_simd(prev)
     oracle.set_simd(True)
-    got = oracle.matmul_kq_mt(w, xq, n, rows, n_tok, rb, quant, 5)
-    oracle.set_simd(prev)
+    try:
+        got = oracle.matmul_kq_mt(w, xq, n, rows, n_tok, rb, quant, 5)
+    finally:
+        oracle.set_simd(prev)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
