@@ -6,13 +6,13 @@
 Prints ONE JSON line. The headline (`value`) is the largest single-GPU
 configuration: a routed-MoE chunk layer of 16 tokens,
 hidden 4096, 128 Q2_K experts of FFN 1536, top-8 by a softmax router, run
-through the grouped path (router_logits_q8 -> moe_route_group -> grouped
-gate/up -> quantize -> grouped down -> slot sum). `value` is that layer's
+through the expert-indexed grouped path (router_logits_q8 -> moe_route ->
+grouped gate/up -> quantize -> grouped down -> slot sum). `value` is that layer's
 algorithmic HBM GB/s: the weight bytes of the distinct experts it touches
 (each once), the router weights and the activations in and out, divided by
 the layer time. A step is one layer; exactly K steps are timed. `roofline`
 is the layer's dominant kernel, the grouped gate/up stage
-(moe_grouped_mmq_kq_kernel<0, true>), timed on its own with HIP events over
+(moe_grouped_mmq_kq_kernel<0, true, ExpertGroups>), timed on its own with HIP events over
 K launches on pre-routed chunks. Every other configuration is reported
 under "results":
   c1  Q4_K 4096x4096 matvec, batch 1
@@ -61,7 +61,7 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 ROTATE_BYTES = 2_200_000_000
 HEADLINE = "c4_moe_chunk16_q2k"
-ROOF_KERNEL = "pk::moe_grouped_mmq_kq_kernel<0u, true>"
+ROOF_KERNEL = "pk::moe_grouped_mmq_kq_kernel<0u, true, pk::ExpertGroups>"
 
 
 def parse_args():
@@ -240,14 +240,17 @@ class LayerBufs:
         self.starts = torch.zeros(self.max_groups + 1, dtype=torch.int32, device="cuda")
         self.pairs = torch.zeros(s.n_tok * n_slots, dtype=torch.int32, device="cuda")
         self.partial = torch.zeros((s.n_tok * n_slots, s.hidden), **f32)
+        self.active = torch.zeros(2 + s.n_expert, dtype=torch.int32, device="cuda")
 
 
 def layer_step(ctx, s, L, B, descs, shared, path):
     """One layer per call. path: "plain" (reference entry points with device
-    routing), "grouped" (router_logits_q8 + moe_route_group + the grouped
-    stages + moe_slot_sum[_bias]: six launches), "grouped_split" (the same
-    grouped stages behind the reference's separate router, select, pointer and
-    CSR entry points: nine or ten), "fused" (router_logits_q8 +
+    routing), "grouped" (router_logits_q8 + moe_route + the expert-indexed
+    grouped stages + moe_slot_sum[_bias]: six launches), "grouped_csr"
+    (router_logits_q8 + moe_route_group + the CSR grouped stages, partial
+    zeroed by a fill kernel, + moe_slot_sum[_bias]: seven), "grouped_split"
+    (the CSR grouped stages behind the reference's separate router, select,
+    pointer and CSR entry points: ten or eleven), "fused" (router_logits_q8 +
     moe_pair_routed + moe_down_f32: three launches) or "fused_q"
     (router_logits_q8 + moe_pair_routed + quantize_q8_k + moe_down_biased:
     four; for wide mid rows, where every fused-down block re-quantizing the
@@ -276,11 +279,26 @@ def layer_step(ctx, s, L, B, descs, shared, path):
             return
         if path == "grouped":
             K.router_logits_q8(B.logits, B.xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
+            K.moe_route(sel, B.rw, B.ptrs, B.slot_w, B.active, B.logits, None, s.n_expert, s.k_used, 1.0, 1, desc,
+                        sh, s.n_tok)
+            K.moe_pair_swiglu_experts(B.mid, sel, B.active, B.slot_w, B.xq, desc, s.n_expert, sh, s.n_tok, s.k_used,
+                                      s.hidden, s.ffn, s.gate_row_bytes, s.gate_quant, s.act_op)
+            K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            K.moe_down_experts(B.partial, sel, B.active, B.midq, desc, s.n_expert, sh, s.n_tok, s.k_used, s.ffn,
+                               s.hidden, s.down_row_bytes, s.down_quant)
+            if s.biases:
+                K.moe_slot_sum_bias(B.out, B.partial, B.ptrs, B.slot_w, s.hidden, n_slots, s.n_tok)
+            else:
+                K.moe_slot_sum(B.out, B.partial, s.hidden, n_slots, s.n_tok)
+            return
+        if path == "grouped_csr":
+            K.router_logits_q8(B.logits, B.xq, x, b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
             K.moe_route_group(sel, B.rw, B.ptrs, B.slot_w, B.gptrs, B.starts, B.pairs, B.logits, None, s.n_expert,
                               s.k_used, 1.0, 1, desc, sh, s.n_tok, B.max_groups)
             K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, n_slots,
                                       B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
             K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            B.partial.zero_()  # the CSR stage writes only listed pairs (the reference zeroes, elib:8481-8482)
             K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, n_slots,
                                B.max_groups, s.down_row_bytes, s.down_quant)
             if s.biases:
@@ -299,6 +317,7 @@ def layer_step(ctx, s, L, B, descs, shared, path):
             K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, n_slots,
                                       B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
             K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * n_slots)
+            B.partial.zero_()
             K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, n_slots,
                                B.max_groups, s.down_row_bytes, s.down_quant)
             K.moe_slot_sum(B.out, B.partial, s.hidden, n_slots, s.n_tok)
@@ -380,17 +399,17 @@ def grouped_stage_timing(ctx, s, L, descs, shared, steps, warmup):
     xs = ctx["synth"].activations(n_route * s.n_tok, s.hidden, ctx["synth"].rng_for(47, s.name))
     xs = torch.from_numpy(xs).cuda().view(n_route, s.n_tok, s.hidden)
     distinct = []
+    sh_of = (lambda i: shared[i % n_banks]) if shared else (lambda i: None)
     for i, B in enumerate(Bs):
         b = L.banks[i % n_banks]
         K.router_logits_q8(B.logits, B.xq, xs[i], b["router_w"], b["router_b"], s.hidden, s.n_expert, s.n_tok)
-        K.moe_route_group(B.sel_all[0], B.rw, B.ptrs, B.slot_w, B.gptrs, B.starts, B.pairs, B.logits, None,
-                          s.n_expert, s.k_used, 1.0, 1, descs[i % n_banks], shared[i % n_banks] if shared else None,
-                          s.n_tok, B.max_groups)
-        K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, B.n_slots,
-                                  B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+        K.moe_route(B.sel_all[0], B.rw, B.ptrs, B.slot_w, B.active, B.logits, None, s.n_expert, s.k_used, 1.0, 1,
+                    descs[i % n_banks], sh_of(i), s.n_tok)
+        K.moe_pair_swiglu_experts(B.mid, B.sel_all[0], B.active, B.slot_w, B.xq, descs[i % n_banks], s.n_expert,
+                                  sh_of(i), s.n_tok, s.k_used, s.hidden, s.ffn, s.gate_row_bytes, s.gate_quant,
+                                  s.act_op)
         K.quantize_q8_k(B.midq, B.mid, s.ffn, s.n_tok * B.n_slots)
-        st = B.starts.cpu().numpy()
-        distinct.append(int(np.count_nonzero(np.diff(st))))
+        distinct.append(len(np.unique(B.sel_all[0].cpu().numpy())) + (1 if s.shared else 0))
     d = float(np.mean(distinct))
     n_pairs = s.n_tok * s.n_slots
     nb_in, nb_mid = fm.q8k_blocks(s.hidden), fm.q8k_blocks(s.ffn)
@@ -398,18 +417,19 @@ def grouped_stage_timing(ctx, s, L, descs, shared, steps, warmup):
 
     def pair(i):
         B = Bs[i % n_route]
-        K.moe_pair_swiglu_grouped(B.mid, B.gptrs, B.starts, B.pairs, B.slot_w, B.xq, s.hidden, s.ffn, B.n_slots,
-                                  B.max_groups, s.gate_row_bytes, s.gate_quant, s.act_op)
+        K.moe_pair_swiglu_experts(B.mid, B.sel_all[0], B.active, B.slot_w, B.xq, descs[i % n_route % n_banks],
+                                  s.n_expert, sh_of(i % n_route), s.n_tok, s.k_used, s.hidden, s.ffn,
+                                  s.gate_row_bytes, s.gate_quant, s.act_op)
 
     def down(i):
         B = Bs[i % n_route]
-        K.moe_down_grouped(B.partial, B.gptrs, B.starts, B.pairs, B.midq, s.ffn, s.hidden, B.n_slots,
-                           B.max_groups, s.down_row_bytes, s.down_quant)
+        K.moe_down_experts(B.partial, B.sel_all[0], B.active, B.midq, descs[i % n_route % n_banks], s.n_expert,
+                           sh_of(i % n_route), s.n_tok, s.k_used, s.ffn, s.hidden, s.down_row_bytes, s.down_quant)
 
     q = s.gate_quant
-    stages = (("gate_up", pair, f"pk::moe_grouped_mmq_kq_kernel<{q}u, true>",
+    stages = (("gate_up", pair, f"pk::moe_grouped_mmq_kq_kernel<{q}u, true, pk::ExpertGroups>",
                d * 2 * s.ffn * s.gate_row_bytes + n_pairs * nb_in * 292 + n_pairs * s.ffn * 4),
-              ("down", down, f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false>",
+              ("down", down, f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false, pk::ExpertGroups>",
                d * s.hidden * s.down_row_bytes + n_pairs * nb_mid * 292 + n_pairs * s.hidden * 4))
     for name, fn, kernel, alg in stages:
         tm = ctx["timer"].run(fn, max(steps, n_route), warmup)
@@ -420,6 +440,28 @@ def grouped_stage_timing(ctx, s, L, descs, shared, steps, warmup):
         out[name]["frac"] = out[name]["GBps"] / HBM_PEAK_GBS
     del Bs
     return out
+
+
+def stream_chain(ctx, sizes, reps: int = 20) -> dict:
+    """The size-matched streaming ceiling of a chain of launches: pulsar_bw_read
+    over `sizes` bytes, one launch per size in order (the bytes and launch
+    count of a decode configuration's kernels), rotating over >= 2.2 GB of
+    regions per size so no launch reads cached data. Returns the chain's
+    time and its GB/s."""
+    torch, K = ctx["torch"], ctx["K"]
+    sizes = [max(256, int(n) // 256 * 256) for n in sizes]
+    total = sum(sizes)
+    n_reg = max(2, -(-ROTATE_BYTES // total))
+    bufs = [torch.ones(n_reg * n // 4, dtype=torch.float32, device="cuda") for n in sizes]
+    sink = torch.zeros(4, dtype=torch.float32, device="cuda")
+
+    def step(i):
+        for b, n in zip(bufs, sizes):
+            K.bw_read(b.data_ptr() + (i % n_reg) * n, n, sink)
+
+    ms = ctx["timer"].run(step, max(reps, n_reg), 3)["ms"]
+    del bufs
+    return {"bytes": total, "launches": len(sizes), "us": ms * 1e3, "GBps": total / (ms * 1e-3) / 1e9}
 
 
 def stream_ceiling(ctx, nbytes: int, reps: int = 10) -> float:
@@ -545,18 +587,22 @@ def pmc_run(ctx, which: str):
     algorithmic bytes per dispatch of its main kernels, the figures the
     counters are compared with."""
     torch, K, synth, fm = ctx["torch"], ctx["K"], ctx["synth"], ctx["fm"]
-    names = ["c2_chunk16", "c3", "c4_q2k", "c4_iq2xxs", "c5_b64"] if which == "all" else which.split(",")
+    names = (["c1", "c2_chunk16", "c3", "c4_q2k", "c4_iq2xxs", "c5_b1", "c5_b64"] if which == "all"
+             else which.split(","))
     specs = {"c3": (synth.C3, "fused"), "c4_q2k": (synth.C4_Q2K, "grouped"),
-             "c4_iq2xxs": (synth.C4_IQ2, "grouped"), "c5_b64": (synth.C5_B64, "grouped")}
+             "c4_iq2xxs": (synth.C4_IQ2, "grouped"), "c5_b1": (synth.C5_B1, "fused_q"),
+             "c5_b64": (synth.C5_B64, "grouped")}
     for name in names:
         print(f"pmc-run {name}", flush=True)
-        if name == "c2_chunk16":
-            q, rows, cols = fm.QUANT_Q6_K, 8192, 4096
+        if name in ("c1", "c2_chunk16"):
+            q, rows, cols = (fm.QUANT_Q4_K, 4096, 4096) if name == "c1" else (fm.QUANT_Q6_K, 8192, 4096)
             w = synth.quant_matrix(q, rows, cols, synth.rng_for(11, "pmc"))
             copies = dev_copies(torch, w, 1_000_000_000)
             rb = fm.row_bytes(q, cols)
             alg = {}
-            for n_tok, kern in ((1, "pk::matvec_kernel<4u, 1u, 1u, 1u, 6u>"), (16, "pk::mmq_gemm_kernel<4u, 2u, 4u, 1u, 2u>")):
+            runs = (((1, "pk::matvec_kernel<2u, 1u, 1u, 1u, 6u>"),) if name == "c1" else
+                    ((1, "pk::matvec_kernel<4u, 1u, 1u, 1u, 6u>"), (16, "pk::mmq_gemm_kernel<4u, 2u, 4u, 1u, 2u>")))
+            for n_tok, kern in runs:
                 x = torch.from_numpy(synth.activations(n_tok, cols, synth.rng_for(12, "pmc"))).cuda()
                 xq = torch.zeros(n_tok * fm.q8k_blocks(cols) * 292, dtype=torch.uint8, device="cuda")
                 K.quantize_q8_k(xq, x, cols, n_tok)
@@ -587,10 +633,17 @@ def pmc_run(ctx, which: str):
         router = s.n_expert * s.hidden * 4 + s.n_tok * s.hidden * 4 + s.n_tok * s.n_expert * 4 + s.n_tok * nb_in * 292
         if path == "grouped":
             alg = {f"pk::router_logits_q8_kernel<4u>": router,
-                   f"pk::moe_grouped_mmq_kq_kernel<{s.gate_quant}u, true>":
+                   f"pk::moe_grouped_mmq_kq_kernel<{s.gate_quant}u, true, pk::ExpertGroups>":
                        gu + n_pairs * nb_in * 292 + n_pairs * s.ffn * 4,
-                   f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false>":
+                   f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false, pk::ExpertGroups>":
                        dn + n_pairs * nb_mid * 292 + n_pairs * s.hidden * 4}
+        elif path == "fused_q":
+            bias_d = d * s.hidden * 4 if s.biases else 0
+            alg = {"pk::router_logits_q8_kernel<1u>": router + (s.n_expert * 4 if s.biases else 0),
+                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, 4u, 2u, 1u>":
+                       gu + s.n_tok * nb_in * 292 + s.n_tok * s.n_expert * 4 + n_pairs * s.ffn * 4,
+                   f"pk::moe_down_kernel<{s.down_quant}u, 1u, 2u, true>":
+                       dn + bias_d + n_pairs * nb_mid * 292 + s.n_tok * s.hidden * 4}
         else:
             alg = {"pk::router_logits_q8_kernel<1u>": router,
                    f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, 4u, 0u, 1u>":
@@ -671,6 +724,8 @@ def main():
         # the same layer through the reference's own (unfused) entry points
         if path.startswith("fused") and on(spec.name + "_unfused"):
             results[spec.name + "_unfused"] = bench_moe(ctx, spec, steps, warmup, "plain")
+    if on(HEADLINE + "_csr"):
+        results[HEADLINE + "_csr"] = bench_moe(ctx, synth.C4_Q2K, steps, warmup, "grouped_csr")
     if on(HEADLINE + "_split"):
         results[HEADLINE + "_split"] = bench_moe(ctx, synth.C4_Q2K, steps, warmup, "grouped_split")
 
@@ -681,6 +736,28 @@ def main():
         ceilings = {"stream_read_4GiB_GBps": stream_ceiling(ctx, 4 << 30),
                     "stream_read_at_roofline_kernel_bytes_GBps": stream_ceiling(ctx, int(roof["alg_bytes_per_launch"])),
                     "roofline_kernel_bytes": int(roof["alg_bytes_per_launch"])}
+    if want is None:
+        # size-matched ceilings of the decode configurations: the same bytes
+        # in the same number of dependent launches, streamed by bw_read
+        c3, c5 = synth.C3, synth.C5_B1
+        chains = {
+            "c1_q4k_4096x4096_decode": [9_458_240],
+            "c2_q6k_8192x4096_decode": [27_562_560],
+            "c3_moe_decode_q4k_q6k": [c3.n_expert * c3.hidden * 4,
+                                      c3.n_slots * 2 * c3.ffn * c3.gate_row_bytes,
+                                      c3.n_slots * c3.hidden * c3.down_row_bytes],
+            "c5_moe_mxfp4_b1": [c5.n_expert * c5.hidden * 4, c5.n_slots * 2 * c5.ffn * c5.gate_row_bytes,
+                                c5.n_slots * c5.ffn * 4, c5.n_slots * c5.hidden * c5.down_row_bytes],
+        }
+        ceilings = dict(ceilings or {})
+        for name, sizes in chains.items():
+            ch = stream_chain(ctx, sizes)
+            ceilings[name] = ch
+            r = results.get(name)
+            if r:
+                us = r.get("us_per_layer", r.get("us_per_launch"))
+                r["ceiling_us"] = ch["us"]
+                r["pct_of_ceiling"] = 100 * ch["us"] / us
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds, ctx)
     if head is None:  # a subset run without the headline
         name, head = next(iter(results.items()))
@@ -717,12 +794,16 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(roof["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": pmc.get("hbm_bytes_per_dispatch"),
+            "traffic": (round(pmc["traffic_over_alg"] * roof["alg_bytes_per_launch"])
+                        if pmc.get("traffic_over_alg") else None),
             "kernel": ROOF_KERNEL,
             "alg_bytes_per_launch": round(roof["alg_bytes_per_launch"]),
             "us_per_launch": round(roof["us_per_launch"], 3),
             "traffic_over_alg": pmc.get("traffic_over_alg"),
             "mfma_busy_frac": pmc.get("mfma_busy_frac"),
+            "counters_source": ("profiles/pmc_counters.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE and SQ counters of "
+                                "this kernel under `bench.py --pmc-run c4_q2k`, scaled by a 256 MiB copy's counts); "
+                                "traffic = that run's HBM/algorithmic ratio x this run's algorithmic bytes"),
         },
         "cpu_baseline": rounded(cpu),
         "stream_ceilings": rounded(ceilings),

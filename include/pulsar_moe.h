@@ -242,6 +242,47 @@ int pulsar_moe_route_group(void *selected, void *weights, void *ptrs, void *slot
                            const pulsar_expert_bank *bank, const pulsar_expert_ptrs *shared,
                            uint32_t n_shared, uint32_t n_tok, uint32_t max_groups);
 
+/* pulsar_router_select (softmax_mode 0 or 1, no sink slots) +
+ * pulsar_moe_route_ptrs in one launch (no reference counterpart: the
+ * reference selects on the device and builds the pointers on the host,
+ * crates/engine/src/lib.rs:7663-7670, 8255-8344). Outputs equal those two
+ * calls': selected / weights [n_tok][k_used], ptrs / slot_weights
+ * [n_tok][k_used + n_shared]. It also writes active, uint32 [2 + n_expert]
+ * (the grouped stages below may read all of it): active[0] = the number of
+ * distinct experts the chunk selects,
+ * active[1] = the number of NULL slots (ids outside [0, n_expert)),
+ * active[2 ..] = the selected expert ids in order of first appearance in
+ * (token, slot) order; the expert-indexed grouped stages below read it.
+ * k_used + n_shared <= 64, k_used <= n_expert <= 1024, n_tok * k_used <=
+ * 2048; bank and shared are host pointers read at launch. */
+int pulsar_moe_route(void *selected, void *weights, void *ptrs, void *slot_weights, void *active,
+                     const void *logits, const void *router_bias, uint32_t n_expert, uint32_t k_used,
+                     float weight_scale, uint32_t softmax_mode, const pulsar_expert_bank *bank,
+                     const pulsar_expert_ptrs *shared, uint32_t n_shared, uint32_t n_tok);
+
+/* The grouped stages with one group per expert the chunk selects, found
+ * on the device from pulsar_moe_route's selected and active outputs
+ * instead of a CSR (no reference counterpart: the reference groups on the
+ * host, crates/engine/src/lib.rs:8357-8392). Each routed (token, slot)
+ * pair runs in the group of its expert, shared slot i (s = k_used + i,
+ * weight 1) of every token in a group of its own, exactly as
+ * pulsar_moe_pair_swiglu_grouped / pulsar_moe_down_grouped would for the
+ * same pairs, so the rows they write are bit-identical to those calls'.
+ * Slots whose id is outside [0, n_expert) get rows of 0 in mid (partial),
+ * so every row of mid [n_tok][k_used + n_shared][mid_dim] (partial
+ * [..][out_dim]) is written and partial needs no zeroing. slot_weights
+ * [n_tok][k_used + n_shared]. k_used + n_shared <= 16, n_tok * (k_used +
+ * n_shared) <= 2048, n_expert <= 1024; bank and shared are host pointers. */
+int pulsar_moe_pair_swiglu_experts(void *mid, const void *selected, const void *active,
+                                   const void *slot_weights, const void *xq, const pulsar_expert_bank *bank,
+                                   uint32_t n_expert, const pulsar_expert_ptrs *shared, uint32_t n_shared,
+                                   uint32_t n_tok, uint32_t k_used, uint32_t in_dim, uint32_t mid_dim,
+                                   uint64_t row_bytes, uint32_t quant, uint32_t act_op);
+int pulsar_moe_down_experts(void *partial, const void *selected, const void *active, const void *midq,
+                            const pulsar_expert_bank *bank, uint32_t n_expert, const pulsar_expert_ptrs *shared,
+                            uint32_t n_shared, uint32_t n_tok, uint32_t k_used, uint32_t mid_dim,
+                            uint32_t out_dim, uint64_t row_bytes, uint32_t quant);
+
 /* pulsar_moe_slot_sum + pulsar_moe_down_bias in one launch (no reference
  * counterpart; the same sums in the same order, bit-identical to the two
  * calls). */

@@ -37,6 +37,10 @@ SIGNATURES = {
     "pulsar_moe_route_group": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp,
                                _u32, _u32, _u32],
     "pulsar_moe_slot_sum_bias": [_vp, _vp, _vp, _vp, _u32, _u32, _u32],
+    "pulsar_moe_route": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp, _u32, _u32],
+    "pulsar_moe_pair_swiglu_experts": [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _u32,
+                                       _u64, _u32, _u32],
+    "pulsar_moe_down_experts": [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u64, _u32],
     "pulsar_set_stream": [_vp],
     "pulsar_router_logits_q8": [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32],
     "pulsar_moe_pair_routed": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _f32, _u32, _vp, _vp, _u32,

@@ -735,12 +735,14 @@ constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 12u : 4u;
 // SIMD. Left to itself the compiler spends more (Q2_K pair 164 VGPRs, Q4_K
 // 240, Q5_K 286); with the bound, 152 / 161 / 231, no spills, and the c4
 // layers run 2-4% faster (Q2_K 182 -> 178 us, IQ2_XXS 205 -> 198 us).
-template <uint32_t Q, bool PAIR>
+// G: where the block's group comes from (CsrGroups: the caller's CSR;
+// ExpertGroups: one group per bank expert, its pair list collected into the
+// dynamic LDS at byte lst_off, after the pair tile).
+template <uint32_t Q, bool PAIR, typename G>
 __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_eu(2))) void moe_grouped_mmq_kq_kernel(
-        float *__restrict__ out, const pulsar_expert_ptrs *__restrict__ gptrs, const uint32_t *__restrict__ starts,
-        const uint32_t *__restrict__ pairs, const float *__restrict__ weights,
+        float *__restrict__ out, const G src, const float *__restrict__ weights,
         const pulsar_block_q8_K *__restrict__ act, uint32_t k_blocks, uint32_t lim, uint32_t n_rows,
-        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
+        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax, uint32_t lst_off) {
     using F = GmmqFmt<Q>;
     constexpr uint32_t NM = PAIR ? 2 : 1;
     constexpr bool kIq2 = Q == PULSAR_QUANT_IQ2_XXS;
@@ -762,12 +764,24 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         __syncthreads();
     }
     const uint32_t group = blockIdx.y;
-    const pulsar_expert_ptrs p = gptrs[group];
+    const typename G::Group grp = src.group(group);
+    const pulsar_expert_ptrs &p = grp.p;
     const uint8_t *w0 = PAIR ? (const uint8_t *)p.gate : (const uint8_t *)p.down;
     const uint8_t *w1 = PAIR ? (const uint8_t *)p.up : nullptr;
-    if (!w0 || (PAIR && !w1)) return;
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    const bool nul = grp.is_null();  // block-uniform
+    if (!nul && (!w0 || (PAIR && !w1))) return;
+    uint32_t *lst = (uint32_t *)(acts_lds + lst_off);
+    uint32_t s0, s1;
+    src.range(grp, lst, s0, s1);
     if (s0 >= s1) return;
+    if (nul) {  // unrouted slots: their rows of this block are 0
+        const uint32_t r0 = blockIdx.x * kGqWaves<Q> * 16u, nr = kGqWaves<Q> * 16u;
+        for (uint32_t it = threadIdx.x; it < (s1 - s0) * nr; it += blockDim.x) {
+            const uint32_t pr = src.pair(s0 + it / nr, lst), row = r0 + it % nr;
+            if (row < n_rows) out[((uint64_t)(pr >> 4) * n_used + (pr & 15u)) * n_rows + row] = 0.0f;
+        }
+        return;
+    }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
     const uint32_t rw0 = (blockIdx.x * kGqWaves<Q> + wave) * 16u;  // the wave's first row
@@ -814,7 +828,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
         if (t0 != s0) __syncthreads();  // the previous tile's activations are consumed
-        if (threadIdx.x < m) pr_l[threadIdx.x] = pairs[t0 + threadIdx.x];
+        if (threadIdx.x < m) pr_l[threadIdx.x] = src.pair(t0 + threadIdx.x, lst);
         __syncthreads();
         stage_q8_rows<2>(acts_lds, m, k_blocks, act_bytes, [&](uint32_t j) {
             const uint32_t pr = pr_l[j];
@@ -1140,11 +1154,15 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     }
 }
 
-// Grouped MoE stages of Q2_K / IQ2_XXS / MXFP4 experts on the matrix cores;
-// -1 for other formats (the caller then uses the lane kernels).
-int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
-                          const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
-                          uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op) {
+// Grouped MoE stages of Q2_K, IQ2_XXS, MXFP4, Q4_K, Q5_K and Q6_K experts
+// on the matrix cores; -1 for the other formats (the caller then uses the
+// lane kernels of moe.hip). `src` is the group source (CsrGroups or
+// ExpertGroups), n_group the grid's group count; lst_bytes the LDS the
+// source's pair list needs (0 for the caller's CSR).
+template <typename G>
+int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const G &src, const float *weights,
+                          const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows, uint32_t n_used,
+                          uint32_t n_group, uint64_t row_bytes, uint32_t act_op, uint32_t lst_bytes) {
     if (quant != PULSAR_QUANT_Q2_K && quant != PULSAR_QUANT_IQ2_XXS && quant != PULSAR_QUANT_MXFP4 &&
         quant != PULSAR_QUANT_Q4_K && quant != PULSAR_QUANT_Q5_K && quant != PULSAR_QUANT_Q6_K)
         return -1;
@@ -1157,13 +1175,13 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
     if (per_pair > budget) return -1;  // one pair's row does not fit: lane kernels
     uint32_t pmax = budget / per_pair;
     pmax = pmax < kGqPairs ? pmax : kGqPairs;
-    const size_t lds = (size_t)pmax * per_pair;
+    const uint32_t lst_off = (pmax * per_pair + 15u) & ~15u;
+    const size_t lds = (size_t)lst_off + lst_bytes;
 #define PK_GQ(Q, P)                                                                                              \
-    hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P>),                                                        \
+    hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P, G>),                                                     \
                        dim3((n_rows + 16u * kGqWaves<Q> - 1u) / (16u * kGqWaves<Q>), n_group),                     \
-                       dim3(64u * kGqWaves<Q>), lds, pk::stream(), out,                                           \
-                       (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs, weights, \
-                       act, k_blocks, lim, n_rows, n_used, row_bytes, act_op, pmax)
+                       dim3(64u * kGqWaves<Q>), lds, pk::stream(), out, src, weights, act, k_blocks, lim, n_rows, \
+                       n_used, row_bytes, act_op, pmax, lst_off)
     if (quant == PULSAR_QUANT_Q2_K && pair)
         PK_GQ(PULSAR_QUANT_Q2_K, true);
     else if (quant == PULSAR_QUANT_Q2_K)
@@ -1191,5 +1209,11 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gpt
 #undef PK_GQ
     return launch_ok(pair ? "moe pair swiglu grouped (mfma) launch" : "moe down grouped (mfma) launch");
 }
+template int launch_grouped_mmq_kq<CsrGroups>(bool, uint32_t, float *, const CsrGroups &, const float *,
+                                              const pulsar_block_q8_K *, uint32_t, uint32_t, uint32_t, uint32_t,
+                                              uint64_t, uint32_t, uint32_t);
+template int launch_grouped_mmq_kq<ExpertGroups>(bool, uint32_t, float *, const ExpertGroups &, const float *,
+                                                 const pulsar_block_q8_K *, uint32_t, uint32_t, uint32_t, uint32_t,
+                                                 uint64_t, uint32_t, uint32_t);
 
 }  // namespace pk

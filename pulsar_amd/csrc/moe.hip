@@ -13,6 +13,7 @@
 // activations are staged in LDS once, and each wave streams row passes of
 // the expert, dotting each pass with every pair.
 #include "pk_rowdot.h"
+#include "pk_route.h"
 
 namespace pk {
 
@@ -126,10 +127,10 @@ constexpr uint32_t kGrpMaxPairs = 16u;   // pairs staged per round
 // layout, `blocks` super-blocks per row) and their pair ids into pr_l.
 // DOWN: the row is the (token, slot)'s mid row, else the token's row.
 // Ends with a block barrier.
-template <bool DOWN>
-PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const uint32_t *pairs, uint32_t c0, uint32_t np,
-                            const pulsar_block_q8_K *src, uint32_t blocks, uint32_t n_used) {
-    for (uint32_t j = threadIdx.x; j < np; j += blockDim.x) pr_l[j] = pairs[c0 + j];
+template <bool DOWN, typename G>
+PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const G &grp, const uint32_t *lst, uint32_t c0,
+                            uint32_t np, const pulsar_block_q8_K *src, uint32_t blocks, uint32_t n_used) {
+    for (uint32_t j = threadIdx.x; j < np; j += blockDim.x) pr_l[j] = grp.pair(c0 + j, lst);
     __syncthreads();
     stage_q8_rows<2>(acts, np, blocks, blocks * kActLdsPitch, [&](uint32_t j) {
         const uint32_t pr = pr_l[j];
@@ -139,28 +140,47 @@ PK_DEV void stage_pair_acts(uint8_t *acts, uint32_t *pr_l, const uint32_t *pairs
     __syncthreads();
 }
 
+// The NULL group's pairs (ExpertGroups): output rows [r0, r0 + nr) of each
+// written as 0.
+template <typename G>
+PK_DEV void zero_group_rows(float *out, const G &grp, const uint32_t *lst, uint32_t s0, uint32_t s1, uint32_t r0,
+                            uint32_t nr, uint32_t n_rows, uint32_t n_used) {
+    for (uint32_t it = threadIdx.x; it < (s1 - s0) * nr; it += blockDim.x) {
+        const uint32_t pr = grp.pair(s0 + it / nr, lst), row = r0 + it % nr;
+        if (row < n_rows) out[((uint64_t)(pr >> 4) * n_used + (pr & 15u)) * n_rows + row] = 0.0f;
+    }
+}
+
 // Grouped kernels: one block per (row block, expert group). The group's
 // pair activations are staged in LDS once (in rounds of `pmax` pairs);
 // every wave streams PK_GRP_PPW row passes of the expert, the next pass's
 // weight loads issued before the current pass is dotted with each pair.
-template <uint32_t Q, uint32_t UPLMAX>
+template <uint32_t Q, uint32_t UPLMAX, typename G>
 __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
-        float *__restrict__ mid, const pulsar_expert_ptrs *__restrict__ gptrs,
-        const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
-        const float *__restrict__ weights, const pulsar_block_q8_K *__restrict__ xq,
-        uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2, uint32_t in_blocks, uint32_t mid_dim,
-        uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax) {
+        float *__restrict__ mid, const G grp, const float *__restrict__ weights,
+        const pulsar_block_q8_K *__restrict__ xq, uint32_t n_units, uint32_t nblk32, uint32_t lpr_log2,
+        uint32_t in_blocks, uint32_t mid_dim, uint32_t n_used, uint64_t row_bytes, uint32_t act_op, uint32_t pmax,
+        uint32_t lst_off) {
     PK_FMT_LUT(Q)
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
-    const pulsar_expert_ptrs p = gptrs[group];
-    if (!p.gate || !p.up) return;
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    const typename G::Group gr = grp.group(group);
+    const pulsar_expert_ptrs &p = gr.p;
+    const bool nul = gr.is_null();
+    if (!nul && (!p.gate || !p.up)) return;
+    uint32_t *lst = (uint32_t *)(acts_lds + lst_off);
+    uint32_t s0, s1;
+    grp.range(gr, lst, s0, s1);
     if (s0 >= s1) return;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t n_pass = (mid_dim + rpp - 1u) / rpp;
+    if (nul) {
+        const uint32_t nr = kWaves * PK_GRP_PPW * rpp;
+        zero_group_rows(mid, grp, lst, s0, s1, blockIdx.x * nr, nr, mid_dim, n_used);
+        return;
+    }
     const uint32_t pass0 = (blockIdx.x * kWaves + threadIdx.x / 64u) * PK_GRP_PPW;
     const uint32_t act_bytes = in_blocks * kActLdsPitch;
     auto row_of = [&](uint32_t pass) {
@@ -177,7 +197,7 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
             load_row_w<Q, UPLMAX>(as_global(p.gate) + (uint64_t)row_of(pass0) * row_bytes, rg, wg);
             load_row_w<Q, UPLMAX>(as_global(p.up) + (uint64_t)row_of(pass0) * row_bytes, rg, wu);
         }
-        stage_pair_acts<false>(acts_lds, pr_l, pairs, c0, np, xq, in_blocks, n_used);
+        stage_pair_acts<false>(acts_lds, pr_l, grp, lst, c0, np, xq, in_blocks, n_used);
         for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
             const uint32_t pass = pass0 + k;
             if (pass >= n_pass) break;  // wave-uniform
@@ -220,24 +240,31 @@ __global__ __launch_bounds__(256) void moe_pair_grouped_kernel(
     }
 }
 
-template <uint32_t Q, uint32_t UPLMAX>
+template <uint32_t Q, uint32_t UPLMAX, typename G>
 __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
-        float *__restrict__ partial, const pulsar_expert_ptrs *__restrict__ gptrs,
-        const uint32_t *__restrict__ starts, const uint32_t *__restrict__ pairs,
-        const pulsar_block_q8_K *__restrict__ midq, uint32_t n_units, uint32_t nblk32,
-        uint32_t lpr_log2, uint32_t mid_blocks, uint32_t out_dim, uint32_t n_used,
-        uint64_t row_bytes, uint32_t pmax) {
+        float *__restrict__ partial, const G grp, const pulsar_block_q8_K *__restrict__ midq, uint32_t n_units,
+        uint32_t nblk32, uint32_t lpr_log2, uint32_t mid_blocks, uint32_t out_dim, uint32_t n_used,
+        uint64_t row_bytes, uint32_t pmax, uint32_t lst_off) {
     PK_FMT_LUT(Q)
     extern __shared__ __align__(16) uint8_t acts_lds[];
     __shared__ uint32_t pr_l[kGrpMaxPairs];
     const uint32_t group = blockIdx.y;
-    const pulsar_expert_ptrs p = gptrs[group];
-    if (!p.down) return;
-    const uint32_t s0 = starts[group], s1 = starts[group + 1];
+    const typename G::Group gr = grp.group(group);
+    const pulsar_expert_ptrs &p = gr.p;
+    const bool nul = gr.is_null();
+    if (!nul && !p.down) return;
+    uint32_t *lst = (uint32_t *)(acts_lds + lst_off);
+    uint32_t s0, s1;
+    grp.range(gr, lst, s0, s1);
     if (s0 >= s1) return;
     const RowGeom rg = row_geom(n_units, nblk32, lpr_log2);
     const uint32_t rpp = 64u >> lpr_log2;
     const uint32_t n_pass = (out_dim + rpp - 1u) / rpp;
+    if (nul) {
+        const uint32_t nr = kWaves * PK_GRP_PPW * rpp;
+        zero_group_rows(partial, grp, lst, s0, s1, blockIdx.x * nr, nr, out_dim, n_used);
+        return;
+    }
     const uint32_t pass0 = (blockIdx.x * kWaves + threadIdx.x / 64u) * PK_GRP_PPW;
     const uint32_t act_bytes = mid_blocks * kActLdsPitch;
     auto row_of = [&](uint32_t pass) {
@@ -252,7 +279,7 @@ __global__ __launch_bounds__(256) void moe_down_grouped_kernel(
             __syncthreads();
             load_row_w<Q, UPLMAX>(as_global(p.down) + (uint64_t)row_of(pass0) * row_bytes, rg, w);
         }
-        stage_pair_acts<true>(acts_lds, pr_l, pairs, c0, np, midq, mid_blocks, n_used);
+        stage_pair_acts<true>(acts_lds, pr_l, grp, lst, c0, np, midq, mid_blocks, n_used);
         for (uint32_t k = 0; k < PK_GRP_PPW; k++) {
             const uint32_t pass = pass0 + k;
             if (pass >= n_pass) break;  // wave-uniform
@@ -473,42 +500,46 @@ struct DownLaunch {
     }
 };
 
+template <typename G>
 struct PairGroupedLaunch {
     void *mid;
-    const void *gptrs, *starts, *pairs, *weights, *xq;
+    G grp;
+    const void *weights, *xq;
     uint32_t mid_dim, n_used, n_group, act_op;
     uint64_t row_bytes;
     Geo g;
+    uint32_t lst_bytes;
     template <uint32_t Q, uint32_t U>
     int run() {
         const uint32_t rpb = kWaves * PK_GRP_PPW * (64u >> g.l2);
         const dim3 grid((mid_dim + rpb - 1u) / rpb, n_group);
         const uint32_t pmax = grouped_pmax(g.blocks);
-        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U>), grid, dim3(256), pmax * g.blocks * kActLdsPitch,
-                           pk::stream(), (float *)mid, (const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts,
-                           (const uint32_t *)pairs, (const float *)weights,
-                           (const pulsar_block_q8_K *)xq, g.n_units, g.nblk32, g.l2, g.blocks,
-                           mid_dim, n_used, row_bytes, act_op, pmax);
+        const uint32_t lst_off = pmax * g.blocks * kActLdsPitch;
+        hipLaunchKernelGGL((moe_pair_grouped_kernel<Q, U, G>), grid, dim3(256), lst_off + lst_bytes, pk::stream(),
+                           (float *)mid, grp, (const float *)weights, (const pulsar_block_q8_K *)xq, g.n_units,
+                           g.nblk32, g.l2, g.blocks, mid_dim, n_used, row_bytes, act_op, pmax, lst_off);
         return launch_ok("moe pair swiglu grouped launch");
     }
 };
 
+template <typename G>
 struct DownGroupedLaunch {
     void *partial;
-    const void *gptrs, *starts, *pairs, *midq;
+    G grp;
+    const void *midq;
     uint32_t out_dim, n_used, n_group;
     uint64_t row_bytes;
     Geo g;
+    uint32_t lst_bytes;
     template <uint32_t Q, uint32_t U>
     int run() {
         const uint32_t rpb = kWaves * PK_GRP_PPW * (64u >> g.l2);
         const dim3 grid((out_dim + rpb - 1u) / rpb, n_group);
         const uint32_t pmax = grouped_pmax(g.blocks);
-        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U>), grid, dim3(256), pmax * g.blocks * kActLdsPitch,
-                           pk::stream(), (float *)partial, (const pulsar_expert_ptrs *)gptrs,
-                           (const uint32_t *)starts, (const uint32_t *)pairs,
-                           (const pulsar_block_q8_K *)midq, g.n_units, g.nblk32, g.l2, g.blocks,
-                           out_dim, n_used, row_bytes, pmax);
+        const uint32_t lst_off = pmax * g.blocks * kActLdsPitch;
+        hipLaunchKernelGGL((moe_down_grouped_kernel<Q, U, G>), grid, dim3(256), lst_off + lst_bytes, pk::stream(),
+                           (float *)partial, grp, (const pulsar_block_q8_K *)midq, g.n_units, g.nblk32, g.l2,
+                           g.blocks, out_dim, n_used, row_bytes, pmax, lst_off);
         return launch_ok("moe down grouped launch");
     }
 };
@@ -561,11 +592,72 @@ extern "C" int pulsar_moe_down_biased(void *out, const void *ptrs, const void *w
 // (pulsar_kernels.cu:3488-3492, 3541-3547): in_dim (pair) and mid_dim (down)
 // multiples of 256, n_used <= 16 (4-bit slot field in `pairs`).
 namespace pk {
-// mmq.hip: the grouped stages of Q2_K / IQ2_XXS / MXFP4 experts on the
-// matrix cores; -1 for other formats
-int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const void *gptrs, const void *starts,
-                          const void *pairs, const float *weights, const pulsar_block_q8_K *act, uint32_t k_dim,
-                          uint32_t n_rows, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t act_op);
+// mmq.hip: the grouped stages of Q2_K / IQ2_XXS / MXFP4 / Q4_K / Q5_K / Q6_K
+// experts on the matrix cores; -1 for other formats
+template <typename G>
+int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const G &src, const float *weights,
+                          const pulsar_block_q8_K *act, uint32_t k_dim, uint32_t n_rows, uint32_t n_used,
+                          uint32_t n_group, uint64_t row_bytes, uint32_t act_op, uint32_t lst_bytes);
+extern template int launch_grouped_mmq_kq<CsrGroups>(bool, uint32_t, float *, const CsrGroups &, const float *,
+                                                     const pulsar_block_q8_K *, uint32_t, uint32_t, uint32_t,
+                                                     uint32_t, uint64_t, uint32_t, uint32_t);
+extern template int launch_grouped_mmq_kq<ExpertGroups>(bool, uint32_t, float *, const ExpertGroups &,
+                                                        const float *, const pulsar_block_q8_K *, uint32_t, uint32_t,
+                                                        uint32_t, uint32_t, uint64_t, uint32_t, uint32_t);
+
+// The grouped gate / up stage for either group source: the matrix-core
+// kernel where the format has one, else the lane kernels.
+template <typename G>
+static int pair_grouped(void *mid, const G &grp, const void *weights, const void *xq, uint32_t in_dim,
+                        uint32_t mid_dim, uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t quant,
+                        uint32_t act_op, uint32_t lst_bytes) {
+#ifndef PK_GRP_LANE_ONLY
+    {
+        const int r = launch_grouped_mmq_kq(true, quant, (float *)mid, grp, (const float *)weights,
+                                            (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group,
+                                            row_bytes, act_op, lst_bytes);
+        if (r >= 0) return r;
+    }
+#endif
+    const Geo g = geo_for(quant, in_dim);
+    PairGroupedLaunch<G> f{mid, grp, weights, xq, mid_dim, n_used, n_group, act_op, row_bytes, g, lst_bytes};
+    if (!quant_ok(quant)) return reject("moe pair swiglu grouped (quant)");
+    return with_format<4>(quant, g.upl, f);
+}
+
+template <typename G>
+static int down_grouped(void *partial, const G &grp, const void *midq, uint32_t mid_dim, uint32_t out_dim,
+                        uint32_t n_used, uint32_t n_group, uint64_t row_bytes, uint32_t quant, uint32_t lst_bytes) {
+#ifndef PK_GRP_LANE_ONLY
+    {
+        const int r = launch_grouped_mmq_kq(false, quant, (float *)partial, grp, nullptr,
+                                            (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
+                                            row_bytes, 0, lst_bytes);
+        if (r >= 0) return r;
+    }
+#endif
+    const Geo g = geo_for(quant, mid_dim);
+    DownGroupedLaunch<G> f{partial, grp, midq, out_dim, n_used, n_group, row_bytes, g, lst_bytes};
+    if (!quant_ok(quant)) return reject("moe down grouped (quant)");
+    return with_format<4>(quant, g.upl, f);
+}
+
+// ExpertGroups from the entry points' arguments (bank and shared are host
+// pointers read here).
+static ExpertGroups expert_groups(const void *selected, const void *active, const pulsar_expert_bank *bank,
+                                  uint32_t n_expert, const pulsar_expert_ptrs *shared, uint32_t n_shared,
+                                  uint32_t n_tok, uint32_t k_used) {
+    ExpertGroups G = {};
+    G.sel = (const int32_t *)selected;
+    G.active = (const uint32_t *)active;
+    G.bank = *bank;
+    for (uint32_t i = 0; i < n_shared; i++) G.shared.p[i] = shared[i];
+    G.n_expert = n_expert;
+    G.k_used = k_used;
+    G.n_shared = n_shared;
+    G.n_tok = n_tok;
+    return G;
+}
 }  // namespace pk
 
 extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, const void *starts,
@@ -584,18 +676,8 @@ extern "C" int pulsar_moe_pair_swiglu_grouped(void *mid, const void *gptrs, cons
         n_group > 65535u || row_bytes == 0 ||
         (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI))
         return reject("moe pair swiglu grouped");
-#ifndef PK_GRP_LANE_ONLY
-    {
-        const int r = launch_grouped_mmq_kq(true, quant, (float *)mid, gptrs, starts, pairs, (const float *)weights,
-                                            (const pulsar_block_q8_K *)xq, in_dim, mid_dim, n_used, n_group,
-                                            row_bytes, act_op);
-        if (r >= 0) return r;
-    }
-#endif
-    const Geo g = geo_for(quant, in_dim);
-    PairGroupedLaunch f{mid, gptrs, starts, pairs, weights, xq, mid_dim, n_used, n_group, act_op, row_bytes, g};
-    if (!quant_ok(quant)) return reject("moe pair swiglu grouped (quant)");
-    return with_format<4>(quant, g.upl, f);
+    const CsrGroups grp{(const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs};
+    return pair_grouped(mid, grp, weights, xq, in_dim, mid_dim, n_used, n_group, row_bytes, quant, act_op, 0u);
 }
 
 extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const void *starts,
@@ -608,18 +690,59 @@ extern "C" int pulsar_moe_down_grouped(void *partial, const void *gptrs, const v
         out_dim == 0 || n_used == 0 || n_used > 16u || n_group == 0 || n_group > 65535u ||
         row_bytes == 0)
         return reject("moe down grouped");
-#ifndef PK_GRP_LANE_ONLY
-    {
-        const int r = launch_grouped_mmq_kq(false, quant, (float *)partial, gptrs, starts, pairs, nullptr,
-                                            (const pulsar_block_q8_K *)midq, mid_dim, out_dim, n_used, n_group,
-                                            row_bytes, 0);
-        if (r >= 0) return r;
-    }
-#endif
-    const Geo g = geo_for(quant, mid_dim);
-    DownGroupedLaunch f{partial, gptrs, starts, pairs, midq, out_dim, n_used, n_group, row_bytes, g};
-    if (!quant_ok(quant)) return reject("moe down grouped (quant)");
-    return with_format<4>(quant, g.upl, f);
+    const CsrGroups grp{(const pulsar_expert_ptrs *)gptrs, (const uint32_t *)starts, (const uint32_t *)pairs};
+    return down_grouped(partial, grp, midq, mid_dim, out_dim, n_used, n_group, row_bytes, quant, 0u);
+}
+
+// Shared checks of the expert-indexed grouped entry points.
+static bool experts_args_ok(const void *selected, const void *active, const pulsar_expert_bank *bank,
+                            uint32_t n_expert, const pulsar_expert_ptrs *shared, uint32_t n_shared, uint32_t n_tok,
+                            uint32_t k_used) {
+    return selected && active && bank && n_expert != 0 && n_expert <= 64u * kMaxPerLane && n_tok != 0 &&
+           k_used != 0 && n_shared <= kMaxShared && (n_shared == 0 || shared) && k_used + n_shared <= 16u &&
+           (uint64_t)n_tok * (k_used + n_shared) <= 2048u;
+}
+
+// The grid's group count: every expert the chunk can touch, the shared
+// slots and the NULL group (groups past the touched count are empty).
+static uint32_t expert_grid_groups(uint32_t n_expert, uint32_t n_shared, uint32_t n_tok, uint32_t k_used) {
+    const uint32_t touch = n_tok * k_used < n_expert ? n_tok * k_used : n_expert;
+    return touch + n_shared + 1u;
+}
+
+extern "C" int pulsar_moe_pair_swiglu_experts(void *mid, const void *selected, const void *active,
+                                              const void *slot_weights, const void *xq,
+                                              const pulsar_expert_bank *bank, uint32_t n_expert,
+                                              const pulsar_expert_ptrs *shared, uint32_t n_shared,
+                                              uint32_t n_tok, uint32_t k_used, uint32_t in_dim, uint32_t mid_dim,
+                                              uint64_t row_bytes, uint32_t quant, uint32_t act_op) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    const uint32_t k_mult = quant == PULSAR_QUANT_MXFP4 ? 32u : 256u;
+    if (!mid || !slot_weights || !xq ||
+        !experts_args_ok(selected, active, bank, n_expert, shared, n_shared, n_tok, k_used) || !bank->gate ||
+        !bank->up || in_dim == 0 || in_dim % k_mult != 0 || mid_dim == 0 || row_bytes == 0 ||
+        (act_op != PULSAR_ACT_SILU && act_op != PULSAR_ACT_SWIGLU_OAI))
+        return reject("moe pair swiglu experts");
+    const ExpertGroups grp = expert_groups(selected, active, bank, n_expert, shared, n_shared, n_tok, k_used);
+    return pair_grouped(mid, grp, slot_weights, xq, in_dim, mid_dim, k_used + n_shared,
+                        expert_grid_groups(n_expert, n_shared, n_tok, k_used), row_bytes, quant, act_op,
+                        4u * n_tok * k_used);
+}
+
+extern "C" int pulsar_moe_down_experts(void *partial, const void *selected, const void *active, const void *midq,
+                                       const pulsar_expert_bank *bank, uint32_t n_expert,
+                                       const pulsar_expert_ptrs *shared, uint32_t n_shared, uint32_t n_tok,
+                                       uint32_t k_used, uint32_t mid_dim, uint32_t out_dim, uint64_t row_bytes,
+                                       uint32_t quant) {
+    quant &= ~PULSAR_QUANT_A4_OK;
+    const uint32_t k_mult = quant == PULSAR_QUANT_MXFP4 ? 32u : 256u;
+    if (!partial || !midq || !experts_args_ok(selected, active, bank, n_expert, shared, n_shared, n_tok, k_used) ||
+        !bank->down || mid_dim == 0 || mid_dim % k_mult != 0 || out_dim == 0 || row_bytes == 0)
+        return reject("moe down experts");
+    const ExpertGroups grp = expert_groups(selected, active, bank, n_expert, shared, n_shared, n_tok, k_used);
+    return down_grouped(partial, grp, midq, mid_dim, out_dim, k_used + n_shared,
+                        expert_grid_groups(n_expert, n_shared, n_tok, k_used), row_bytes, quant,
+                        4u * n_tok * k_used);
 }
 
 extern "C" int pulsar_moe_slot_sum(void *out, const void *partial, uint32_t out_dim, uint32_t n_used,

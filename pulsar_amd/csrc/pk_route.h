@@ -281,5 +281,122 @@ PK_DEV SlotRoute route_slot(const float *lg, const float *rbias, uint32_t n_expe
     return r;
 }
 
+// ---- how a grouped block finds its expert group --------------------------
+// Both sources resolve group g to a Group (the expert's pointers and what
+// the group is) with group(); range() then gives the group's (token, slot)
+// pairs (token << 4 | slot, in pair order) through pair(), which a thread
+// may call for any index in [b, e) right after range().
+
+// The reference's grouped contract: a CSR by expert from the caller
+// (gptrs [n_group], starts [n_group + 1], pairs), pulsar_kernels.cu:3483-3591.
+struct CsrGroups {
+    const pulsar_expert_ptrs *gptrs;
+    const uint32_t *starts;
+    const uint32_t *pairs;
+#ifdef PK_CSR_PAD
+    uint8_t pad_[296];
+#endif
+    struct Group {
+        pulsar_expert_ptrs p;
+        uint32_t g;
+        PK_DEV bool is_null() const { return false; }
+    };
+    PK_DEV Group group(uint32_t g) const { return Group{gptrs[g], g}; }
+    PK_DEV void range(const Group &G, uint32_t *, uint32_t &b, uint32_t &e) const {
+        b = starts[G.g];
+        e = starts[G.g + 1u];
+    }
+    PK_DEV uint32_t pair(uint32_t i, const uint32_t *) const { return pairs[i]; }
+};
+
+// One group per expert a chunk touches, in a resident bank, found from the
+// router's selected ids (no CSR). active (written by the router,
+// pulsar_moe_route): [0] = the number of touched experts, [1] = the number
+// of NULL slots, [2 ..] = the touched expert ids (first appearance
+// order). Group g < active[0] is
+// bank expert active[2 + g], its pairs the (token, slot < k_used) whose id
+// is that expert; the next n_shared groups are the shared slots k_used + i
+// of every token; the next is the NULL group, the slots whose id is outside
+// [0, n_expert), whose output rows the grouped kernels write as 0 (an
+// unrouted slot contributes zero, pulsar_kernels.cu:2587-2590, 2635); later
+// groups are empty. A block reads its group with one load and collects its
+// pairs in pair order into an LDS list of up to n_tok * k_used entries.
+// Every thread of the block calls range(), which has no block barrier; the
+// list is read by the block only after its next barrier.
+struct ExpertGroups {
+    const int32_t *sel;      // [n_tok][k_used]
+    const uint32_t *active;  // [2 + touched experts]
+    pulsar_expert_bank bank;
+    SharedSlots shared;
+    uint32_t n_expert, k_used, n_shared, n_tok;
+    struct Group {
+        pulsar_expert_ptrs p;
+        uint32_t kind, e;  // kind 0: routed expert e, 1: shared slot e, 2: NULL, 3: empty
+        int32_t pf[2];     // this lane's selected ids q = lane, lane + 64
+        PK_DEV bool is_null() const { return kind == 2u; }
+    };
+    // active[0], active[1], the group's id and the lane's first selected ids
+    // are requested together (clamped indices; active holds 2 + n_expert
+    // entries), so the block's pair list costs one memory round trip.
+    PK_DEV Group group(uint32_t g) const {
+        const uint32_t total = n_tok * k_used;
+        const uint32_t lane = threadIdx.x & 63u;
+        const uint32_t n_act = active[0], n_nul = active[1];
+        const uint32_t e_g = active[2u + (g < n_expert ? g : n_expert - 1u)];
+        Group G;
+        G.pf[0] = sel[lane < total ? lane : total - 1u];
+        G.pf[1] = sel[lane + 64u < total ? lane + 64u : total - 1u];
+        G.p = pulsar_expert_ptrs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+        G.e = 0u;
+        if (g < n_act) {
+            G.kind = 0u;
+            G.e = e_g;
+            G.p = bank_ptrs(bank, n_expert, (int32_t)e_g);
+        } else if (g < n_act + n_shared) {
+            G.kind = 1u;
+            G.e = g - n_act;
+            G.p = shared.p[G.e];
+        } else {
+            G.kind = g == n_act + n_shared && n_nul != 0u ? 2u : 3u;
+        }
+        return G;
+    }
+    // Every wave scans the selected ids and writes the same list to lst
+    // (ballots, no block barrier); on return the calling wave's writes are
+    // visible to the wave's lanes, so a thread may read any entry of the
+    // list before the block's next barrier. lst holds the pairs [b, e).
+    PK_DEV void range(const Group &G, uint32_t *lst, uint32_t &b, uint32_t &e) const {
+        const uint32_t lane = threadIdx.x & 63u;
+        b = e = 0u;
+        if (G.kind == 3u) return;
+        if (G.kind == 1u) {  // a shared slot: every token
+            const uint32_t sl = k_used + G.e;
+            for (uint32_t t = lane; t < n_tok; t += 64u) lst[t] = (t << 4) | sl;
+            e = n_tok;
+        } else {
+            const bool nul = G.kind == 2u;
+            const int32_t want = (int32_t)G.e;
+            const uint32_t total = n_tok * k_used;
+            uint32_t base = 0u;
+            for (uint32_t q0 = 0; q0 < total; q0 += 64u) {  // wave-uniform
+                const uint32_t q = q0 + lane;
+                const int32_t id = q0 == 0u ? G.pf[0] : q0 == 64u ? G.pf[1] : sel[q < total ? q : total - 1u];
+                const bool hit = q < total && (nul ? (id < 0 || (uint32_t)id >= n_expert) : id == want);
+                const uint64_t bal = __ballot(hit);
+                if (hit) {
+                    const uint32_t t = q / k_used;
+                    lst[base + (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull))] =
+                            (t << 4) | (q - t * k_used);
+                }
+                base += (uint32_t)__builtin_popcountll(bal);
+            }
+            e = base;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    PK_DEV uint32_t pair(uint32_t i, const uint32_t *lst) const { return lst[i]; }
+};
 
 }  // namespace pk

@@ -342,6 +342,84 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
             n_tok * n_slots, n_slots, max_groups);
 }
 
+// router_select (modes 0/1) + route_ptrs in one block of 16 waves, tokens
+// round-robin over the waves: route_lane's top-k and weights per token,
+// then lane k < k_used writes slot k's id, weight, pointers and slot
+// weight, lanes k_used .. k_used + n_shared - 1 the shared slots (weight
+// 1). The same values as route_group_kernel and as the two separate calls.
+// The block also lists the experts the chunk touches, for the
+// expert-indexed grouped stages: active[0] = their count, active[1] = the
+// number of NULL slots (ids outside [0, n_expert)), active[2 ..] = the
+// touched expert ids in order of first appearance in (token, slot) order,
+// the group order of the reference's host CSR (crates/engine/src/lib.rs:
+// 8357-8392). That order also streams faster than ascending ids: ascending
+// ids keep the resident blocks on neighbouring experts, one contiguous
+// slice of the bank (c4 gate / up 88.4 against 83.8 us, same chunks).
+constexpr uint32_t kRouteWaves = 16;
+template <uint32_t J>
+__global__ __launch_bounds__(64 * kRouteWaves) void route_kernel(
+        int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
+        float *__restrict__ slot_w, uint32_t *__restrict__ active, const float *__restrict__ logits,
+        const float *__restrict__ rbias, uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode,
+        pulsar_expert_bank bank, SharedSlots shared, uint32_t n_shared, uint32_t n_tok) {
+    __shared__ uint32_t first_l[64u * kMaxPerLane];  // an expert's first (token, slot) index
+    __shared__ int32_t eid_l[kMaxCsrPairs];           // routed id of (token, slot < k_used)
+    __shared__ uint32_t n_null, wcnt[kRouteWaves];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < n_expert; i += blockDim.x) first_l[i] = UINT32_MAX;
+    if (threadIdx.x == 0) n_null = 0u;
+    __syncthreads();
+    const uint32_t n_slots = k_used + n_shared;
+    uint32_t nulls = 0u;
+    for (uint32_t t = wave; t < n_tok; t += kRouteWaves) {  // wave-uniform
+        int32_t e;
+        float w;
+        route_lane<J>(logits + (uint64_t)t * n_expert, rbias, n_expert, k_used, scale, mode, e, w);
+        const uint64_t i = (uint64_t)t * n_slots + lane;
+        if (lane < k_used) {
+            const uint32_t q = t * k_used + lane;
+            sel[q] = e;
+            rw[q] = w;
+            ptrs[i] = bank_ptrs(bank, n_expert, e);
+            slot_w[i] = w;
+            if (q < kMaxCsrPairs) eid_l[q] = e;
+            if (e >= 0 && (uint32_t)e < n_expert)
+                atomicMin(&first_l[(uint32_t)e], q);
+            else
+                nulls++;
+        } else if (lane < n_slots) {
+            ptrs[i] = shared.p[lane - k_used];
+            slot_w[i] = 1.0f;
+        }
+    }
+    if (nulls) atomicAdd(&n_null, nulls);
+    __syncthreads();
+    // touched experts by first appearance: pair q is its expert's first
+    // one; their ranks among the pairs by ballots and wave offsets
+    const uint32_t total_q = n_tok * k_used;
+    uint32_t base = 0u;
+    for (uint32_t q0 = 0; q0 < total_q; q0 += blockDim.x) {  // block-uniform
+        const uint32_t q = q0 + threadIdx.x;
+        const int32_t e = q < total_q ? eid_l[q] : -1;
+        const bool first = e >= 0 && (uint32_t)e < n_expert && first_l[(uint32_t)e] == q;
+        const uint64_t bal = __ballot(first);
+        if (lane == 0) wcnt[wave] = (uint32_t)__builtin_popcountll(bal);
+        __syncthreads();
+        uint32_t off = base, tot = 0u;
+        for (uint32_t w = 0; w < kRouteWaves; w++) {
+            off += w < wave ? wcnt[w] : 0u;
+            tot += wcnt[w];
+        }
+        if (first) active[2u + off + (uint32_t)__builtin_popcountll(bal & ((1ull << lane) - 1ull))] = (uint32_t)e;
+        base += tot;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        active[0] = base;
+        active[1] = n_null;
+    }
+}
+
 }  // namespace pk
 
 extern "C" int pulsar_moe_route_ptrs(void *ptrs, void *slot_weights, const void *selected,
@@ -406,4 +484,34 @@ extern "C" int pulsar_moe_route_group(void *selected, void *weights, void *ptrs,
         PK_RG(16);
 #undef PK_RG
     return pk::launch_ok("moe route group launch");
+}
+
+extern "C" int pulsar_moe_route(void *selected, void *weights, void *ptrs, void *slot_weights, void *active,
+                                const void *logits, const void *router_bias, uint32_t n_expert, uint32_t k_used,
+                                float weight_scale, uint32_t softmax_mode, const pulsar_expert_bank *bank,
+                                const pulsar_expert_ptrs *shared, uint32_t n_shared, uint32_t n_tok) {
+    if (!selected || !weights || !ptrs || !slot_weights || !active || !logits || !bank || n_tok == 0 ||
+        k_used == 0 || k_used > n_expert || n_expert > 64u * pk::kMaxPerLane || softmax_mode > 1u ||
+        n_shared > pk::kMaxShared || (n_shared && !shared) || k_used + n_shared > 64u ||
+        (uint64_t)n_tok * k_used > pk::kMaxCsrPairs)
+        return pk::reject("moe route");
+    pk::SharedSlots sh = {};
+    for (uint32_t s = 0; s < n_shared; s++) sh.p[s] = shared[s];
+#define PK_RT(J)                                                                                                 \
+    hipLaunchKernelGGL(pk::route_kernel<J>, dim3(1), dim3(64u * pk::kRouteWaves), 0, pk::stream(),              \
+                       (int32_t *)selected, (float *)weights, (pulsar_expert_ptrs *)ptrs, (float *)slot_weights, \
+                       (uint32_t *)active, (const float *)logits, (const float *)router_bias, n_expert, k_used,   \
+                       weight_scale, softmax_mode, *bank, sh, n_shared, n_tok)
+    if (n_expert <= 64u)
+        PK_RT(1);
+    else if (n_expert <= 128u)
+        PK_RT(2);
+    else if (n_expert <= 256u)
+        PK_RT(4);
+    else if (n_expert <= 512u)
+        PK_RT(8);
+    else
+        PK_RT(16);
+#undef PK_RT
+    return pk::launch_ok("moe route launch");
 }

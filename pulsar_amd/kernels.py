@@ -181,6 +181,42 @@ def moe_route_group(selected, weights, ptrs, slot_weights, gptrs, starts, pairs,
         ctypes.cast(arr, ctypes.c_void_p), n_shared, n_tok, max_groups), "moe_route_group")
 
 
+def moe_route(selected, weights, ptrs, slot_weights, active, logits, router_bias, n_expert: int, k_used: int,
+              weight_scale: float, softmax_mode: int, bank: "ExpertBank", shared, n_tok: int) -> None:
+    """router_select (modes 0/1) + moe_route_ptrs in one launch (equal
+    outputs), plus `active` (uint32 [2 + n_expert]): the count of distinct
+    selected experts, the count of NULL slots, the expert ids ascending."""
+    arr, n_shared = _shared_array(shared)
+    _check(_lib.load().pulsar_moe_route(
+        _ptr(selected), _ptr(weights), _ptr(ptrs), _ptr(slot_weights), _ptr(active), _ptr(logits), _ptr(router_bias),
+        n_expert, k_used, weight_scale, softmax_mode, ctypes.byref(bank), ctypes.cast(arr, ctypes.c_void_p),
+        n_shared, n_tok), "moe_route")
+
+
+def moe_pair_swiglu_experts(mid, selected, active, slot_weights, xq, bank: "ExpertBank", n_expert: int, shared,
+                            n_tok: int, k_used: int, in_dim: int, mid_dim: int, row_bytes: int, quant: int,
+                            act_op: int) -> None:
+    """The grouped gate/up stage with one group per selected expert, grouped
+    on the device from moe_route's outputs (rows equal
+    moe_pair_swiglu_grouped's; unrouted slots get rows of 0)."""
+    arr, n_shared = _shared_array(shared)
+    _check(_lib.load().pulsar_moe_pair_swiglu_experts(
+        _ptr(mid), _ptr(selected), _ptr(active), _ptr(slot_weights), _ptr(xq), ctypes.byref(bank), n_expert,
+        ctypes.cast(arr, ctypes.c_void_p), n_shared, n_tok, k_used, in_dim, mid_dim, row_bytes, quant, act_op),
+        "moe_pair_swiglu_experts")
+
+
+def moe_down_experts(partial, selected, active, midq, bank: "ExpertBank", n_expert: int, shared, n_tok: int,
+                     k_used: int, mid_dim: int, out_dim: int, row_bytes: int, quant: int) -> None:
+    """The grouped down stage with one group per selected expert; writes
+    every row of partial (0 for unrouted slots)."""
+    arr, n_shared = _shared_array(shared)
+    _check(_lib.load().pulsar_moe_down_experts(
+        _ptr(partial), _ptr(selected), _ptr(active), _ptr(midq), ctypes.byref(bank), n_expert,
+        ctypes.cast(arr, ctypes.c_void_p), n_shared, n_tok, k_used, mid_dim, out_dim, row_bytes, quant),
+        "moe_down_experts")
+
+
 def _shared_array(shared):
     shared = list(shared or [])
     arr = (_Ptrs6 * max(1, len(shared)))()

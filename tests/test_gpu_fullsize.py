@@ -327,6 +327,22 @@ def test_grouped_chunk_layer_full_shape(dev, spec):
     for j in range(n_slots):
         acc += p[:, j]
     assert np.array_equal(down(out), acc)  # slot sum in slot order
+    # the expert-indexed grouped stages (no CSR) write the same rows
+    sel_e, rw_e = torch.zeros_like(sel), torch.zeros_like(rw)
+    ptrs_e, slot_w_e = torch.zeros_like(ptrs), torch.zeros_like(slot_w)
+    active = torch.zeros(2 + s.n_expert, dtype=torch.int32, device="cuda")
+    K.moe_route(sel_e, rw_e, ptrs_e, slot_w_e, active, logits, None, s.n_expert, s.k_used, 1.0, 1, L.desc(),
+                L.shared(), n_tok)
+    for ga, gb in ((sel, sel_e), (rw, rw_e), (ptrs, ptrs_e), (slot_w, slot_w_e)):
+        assert np.array_equal(down(ga).view(np.uint8), down(gb).view(np.uint8))
+    mid_e = torch.full((n_tok * n_slots, s.ffn), float("nan"), **f32)
+    K.moe_pair_swiglu_experts(mid_e, sel_e, active, slot_w_e, xq_d, L.desc(), s.n_expert, L.shared(), n_tok,
+                              s.k_used, s.hidden, s.ffn, s.gate_row_bytes, s.gate_quant, s.act_op)
+    assert np.array_equal(down(mid_e).view(np.uint32), down(mid).view(np.uint32))
+    partial_e = torch.full((n_tok * n_slots, s.hidden), float("nan"), **f32)
+    K.moe_down_experts(partial_e, sel_e, active, up(midq), L.desc(), s.n_expert, L.shared(), n_tok, s.k_used,
+                       s.ffn, s.hidden, s.down_row_bytes, s.down_quant)
+    assert np.array_equal(down(partial_e).view(np.uint32), down(partial).view(np.uint32))
     if s.biases:
         # down bias, bit-exact against the oracle's formula
         hptrs = oracle.host_ptrs([L.host_slot(int(e)) for e in slots.reshape(-1)])
