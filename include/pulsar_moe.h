@@ -253,8 +253,8 @@ int pulsar_moe_route_group(void *selected, void *weights, void *ptrs, void *slot
  * active[1] = the number of NULL slots (ids outside [0, n_expert)),
  * active[2 ..] = the selected expert ids in order of first appearance in
  * (token, slot) order; the expert-indexed grouped stages below read it.
- * k_used + n_shared <= 64, k_used <= n_expert <= 1024, n_tok * k_used <=
- * 2048; bank and shared are host pointers read at launch. */
+ * k_used + n_shared <= 16, k_used <= n_expert <= 1024, n_tok * (k_used +
+ * n_shared) <= 2048; bank and shared are host pointers read at launch. */
 int pulsar_moe_route(void *selected, void *weights, void *ptrs, void *slot_weights, void *active,
                      const void *logits, const void *router_bias, uint32_t n_expert, uint32_t k_used,
                      float weight_scale, uint32_t softmax_mode, const pulsar_expert_bank *bank,

@@ -1,6 +1,6 @@
 """Builds libpulsar_moe.so (the HIP kernels + C ABI) in-tree for gfx950.
 
-    python -m pulsar_amd.build
+    python -m pulsar_amd.build [--changed]
 
 Each .hip translation unit compiles in parallel to an object under
 pulsar_amd/_build/, then the objects link into pulsar_amd/libpulsar_moe.so.
@@ -56,12 +56,24 @@ def _compile(src: Path, obj: Path) -> None:
         sys.stderr.write("\n".join(noise) + "\n")
 
 
-def build_library(jobs: int | None = None) -> Path:
-    """Compiles every HIP source and links libpulsar_moe.so; returns its path."""
+def _stale(src: Path, obj: Path) -> bool:
+    """True when obj is missing or older than its source or any header it
+    may include (the package's and include/'s)."""
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.h"), *(PKG.parent / "include").glob("*.h")]
+    return obj.stat().st_mtime < max(d.stat().st_mtime for d in deps)
+
+
+def build_library(jobs: int | None = None, changed_only: bool = False) -> Path:
+    """Compiles the HIP sources (all of them, or with changed_only only those
+    whose object is older than the source or a header) and links
+    libpulsar_moe.so; returns its path."""
     BUILD.mkdir(exist_ok=True)
     objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
+    todo = [(CSRC / s, o) for s, o in zip(SOURCES, objs) if not changed_only or _stale(CSRC / s, o)]
     with ThreadPoolExecutor(max_workers=jobs or min(8, len(SOURCES))) as ex:
-        list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+        list(ex.map(lambda so: _compile(*so), todo))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -72,4 +84,4 @@ def build_library(jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    print(build_library())
+    print(build_library(changed_only="--changed" in sys.argv))

@@ -207,23 +207,22 @@ PK_DEV uint32_t group_max_u32(uint32_t v, uint32_t lpt) {
     return (uint32_t)x;
 }
 
-// router_select (modes 0/1) + route_ptrs + group_csr in one block. A wave
+// The routing of route_group_kernel / route_kernel: router_select (modes
+// 0/1) + route_ptrs for every token of the chunk by one block. A wave
 // routes 64 / lpt tokens at once, lpt lanes per token (lane kk of a group
 // holds experts kk J .. kk J + J - 1): every top-k round is a group
 // maximum, the winner is the group's lowest lane holding it (its lowest
 // such expert), which records (expert, prob) for round k in LDS and drops
 // that score to -inf, as topk_wave does for one token per wave. The router
 // weights then follow route_lane's arithmetic from the recorded winners in
-// round order. Every pair's expert is kept in LDS and the CSR is built from
-// those as group_csr_kernel does.
+// round order. Every pair's expert goes to eid_l (routed id, -1 for a NULL
+// slot, -2 - s for shared slot s); the caller's block barrier follows.
 template <uint32_t J>
-__global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
-        int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
-        float *__restrict__ slot_w, pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
-        uint32_t *__restrict__ pairs, const float *__restrict__ logits, const float *__restrict__ rbias,
-        uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode, pulsar_expert_bank bank,
-        SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups, uint32_t lpt) {
-    __shared__ int32_t eid_l[kMaxCsrPairs];  // routed expert, or -2 - s for shared slot s
+PK_DEV void route_tokens(int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
+                         float *__restrict__ slot_w, const float *__restrict__ logits, const float *__restrict__ rbias,
+                         uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode,
+                         const pulsar_expert_bank &bank, const SharedSlots &shared, uint32_t n_shared, uint32_t n_tok,
+                         uint32_t lpt, int32_t *eid_l) {
     __shared__ int32_t win_e[kMaxCsrPairs + 64];  // token t's round-k winner at t k_used + k (+ spare slots)
     __shared__ float win_p[kMaxCsrPairs + 64];    // ... and its prob
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -231,10 +230,26 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
     const uint32_t tpw = 64u / lpt, g0 = lane & ~(lpt - 1u), kk = lane - g0;
     const uint64_t gmask = lpt == 64u ? ~0ull : (1ull << lpt) - 1ull;
     const uint32_t kNegInf = score_key(-INFINITY);
-    // the CSR tables are cleared first (the barrier before the build orders
-    // it), while the logits loads are in flight
-    __shared__ CsrLds T;
-    csr_clear(T);
+    if (lpt == 64u) {  // a token per wave: route_lane's DPP wave maxima
+        for (uint32_t t = wave; t < n_tok; t += kCsrThreads / 64u) {  // wave-uniform
+            int32_t e;
+            float w;
+            route_lane<J>(logits + (uint64_t)t * n_expert, rbias, n_expert, k_used, scale, mode, e, w);
+            const uint64_t i = (uint64_t)t * n_slots + lane;
+            if (lane < k_used) {
+                sel[(uint64_t)t * k_used + lane] = e;
+                rw[(uint64_t)t * k_used + lane] = w;
+                ptrs[i] = bank_ptrs(bank, n_expert, e);
+                slot_w[i] = w;
+                eid_l[i] = e < 0 ? -1 : e;
+            } else if (lane < n_slots) {
+                ptrs[i] = shared.p[lane - k_used];
+                slot_w[i] = 1.0f;
+                eid_l[i] = -2 - (int32_t)(lane - k_used);
+            }
+        }
+        return;
+    }
     for (uint32_t tb = wave * tpw; tb < n_tok; tb += (kCsrThreads / 64u) * tpw) {
         const uint32_t t = tb + lane / lpt;
         const bool t_ok = t < n_tok;
@@ -332,6 +347,25 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
             eid_l[i] = -2 - (int32_t)(kk - k_used);
         }
     }
+}
+
+// router_select (modes 0/1) + route_ptrs + group_csr in one block: the
+// routing of route_tokens, then the CSR built from every pair's expert as
+// group_csr_kernel does (the CSR tables are cleared first, while the
+// logits load).
+template <uint32_t J>
+__global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
+        int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
+        float *__restrict__ slot_w, pulsar_expert_ptrs *__restrict__ gptrs, uint32_t *__restrict__ starts,
+        uint32_t *__restrict__ pairs, const float *__restrict__ logits, const float *__restrict__ rbias,
+        uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode, pulsar_expert_bank bank,
+        SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t max_groups, uint32_t lpt) {
+    __shared__ int32_t eid_l[kMaxCsrPairs];  // routed expert, or -2 - s for shared slot s
+    __shared__ CsrLds T;
+    csr_clear(T);
+    route_tokens<J>(sel, rw, ptrs, slot_w, logits, rbias, n_expert, k_used, scale, mode, bank, shared, n_shared,
+                    n_tok, lpt, eid_l);
+    const uint32_t n_slots = k_used + n_shared;
     __syncthreads();
     auto ptrs_of = [&](uint32_t i) {
         const int32_t e = eid_l[i];
@@ -342,71 +376,53 @@ __global__ __launch_bounds__(kCsrThreads) void route_group_kernel(
             n_tok * n_slots, n_slots, max_groups);
 }
 
-// router_select (modes 0/1) + route_ptrs in one block of 16 waves, tokens
-// round-robin over the waves: route_lane's top-k and weights per token,
-// then lane k < k_used writes slot k's id, weight, pointers and slot
-// weight, lanes k_used .. k_used + n_shared - 1 the shared slots (weight
-// 1). The same values as route_group_kernel and as the two separate calls.
-// The block also lists the experts the chunk touches, for the
+// router_select (modes 0/1) + route_ptrs in one block (the routing of
+// route_tokens: the same values as route_group_kernel and as the two
+// separate calls), then the list of the experts the chunk touches, for the
 // expert-indexed grouped stages: active[0] = their count, active[1] = the
 // number of NULL slots (ids outside [0, n_expert)), active[2 ..] = the
 // touched expert ids in order of first appearance in (token, slot) order,
 // the group order of the reference's host CSR (crates/engine/src/lib.rs:
-// 8357-8392). That order also streams faster than ascending ids: ascending
-// ids keep the resident blocks on neighbouring experts, one contiguous
-// slice of the bank (c4 gate / up 88.4 against 83.8 us, same chunks).
-constexpr uint32_t kRouteWaves = 16;
+// 8357-8392). That order also streams faster than ascending ids, which
+// keep the resident blocks on neighbouring experts, one contiguous slice
+// of the bank (c4 gate / up 88.4 against 83.8 us on the same chunks).
 template <uint32_t J>
-__global__ __launch_bounds__(64 * kRouteWaves) void route_kernel(
+__global__ __launch_bounds__(kCsrThreads) void route_kernel(
         int32_t *__restrict__ sel, float *__restrict__ rw, pulsar_expert_ptrs *__restrict__ ptrs,
         float *__restrict__ slot_w, uint32_t *__restrict__ active, const float *__restrict__ logits,
         const float *__restrict__ rbias, uint32_t n_expert, uint32_t k_used, float scale, uint32_t mode,
-        pulsar_expert_bank bank, SharedSlots shared, uint32_t n_shared, uint32_t n_tok) {
-    __shared__ uint32_t first_l[64u * kMaxPerLane];  // an expert's first (token, slot) index
-    __shared__ int32_t eid_l[kMaxCsrPairs];           // routed id of (token, slot < k_used)
-    __shared__ uint32_t n_null, wcnt[kRouteWaves];
+        pulsar_expert_bank bank, SharedSlots shared, uint32_t n_shared, uint32_t n_tok, uint32_t lpt) {
+    __shared__ int32_t eid_l[kMaxCsrPairs];
+    __shared__ uint32_t first_l[64u * kMaxPerLane];  // an expert's first pair index
+    __shared__ uint32_t n_null, wcnt[kCsrThreads / 64u];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     for (uint32_t i = threadIdx.x; i < n_expert; i += blockDim.x) first_l[i] = UINT32_MAX;
     if (threadIdx.x == 0) n_null = 0u;
+    route_tokens<J>(sel, rw, ptrs, slot_w, logits, rbias, n_expert, k_used, scale, mode, bank, shared, n_shared,
+                    n_tok, lpt, eid_l);
     __syncthreads();
-    const uint32_t n_slots = k_used + n_shared;
+    const uint32_t n = n_tok * (k_used + n_shared);
     uint32_t nulls = 0u;
-    for (uint32_t t = wave; t < n_tok; t += kRouteWaves) {  // wave-uniform
-        int32_t e;
-        float w;
-        route_lane<J>(logits + (uint64_t)t * n_expert, rbias, n_expert, k_used, scale, mode, e, w);
-        const uint64_t i = (uint64_t)t * n_slots + lane;
-        if (lane < k_used) {
-            const uint32_t q = t * k_used + lane;
-            sel[q] = e;
-            rw[q] = w;
-            ptrs[i] = bank_ptrs(bank, n_expert, e);
-            slot_w[i] = w;
-            if (q < kMaxCsrPairs) eid_l[q] = e;
-            if (e >= 0 && (uint32_t)e < n_expert)
-                atomicMin(&first_l[(uint32_t)e], q);
-            else
-                nulls++;
-        } else if (lane < n_slots) {
-            ptrs[i] = shared.p[lane - k_used];
-            slot_w[i] = 1.0f;
-        }
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const int32_t e = eid_l[i];
+        if (e >= 0)
+            atomicMin(&first_l[(uint32_t)e], i);
+        else if (e == -1)
+            nulls++;
     }
     if (nulls) atomicAdd(&n_null, nulls);
     __syncthreads();
-    // touched experts by first appearance: pair q is its expert's first
-    // one; their ranks among the pairs by ballots and wave offsets
-    const uint32_t total_q = n_tok * k_used;
+    // pair i is its expert's first one: their ranks by ballots and wave offsets
     uint32_t base = 0u;
-    for (uint32_t q0 = 0; q0 < total_q; q0 += blockDim.x) {  // block-uniform
-        const uint32_t q = q0 + threadIdx.x;
-        const int32_t e = q < total_q ? eid_l[q] : -1;
-        const bool first = e >= 0 && (uint32_t)e < n_expert && first_l[(uint32_t)e] == q;
+    for (uint32_t i0 = 0; i0 < n; i0 += blockDim.x) {  // block-uniform
+        const uint32_t i = i0 + threadIdx.x;
+        const int32_t e = i < n ? eid_l[i] : -1;
+        const bool first = e >= 0 && first_l[(uint32_t)e] == i;
         const uint64_t bal = __ballot(first);
         if (lane == 0) wcnt[wave] = (uint32_t)__builtin_popcountll(bal);
         __syncthreads();
         uint32_t off = base, tot = 0u;
-        for (uint32_t w = 0; w < kRouteWaves; w++) {
+        for (uint32_t w = 0; w < kCsrThreads / 64u; w++) {
             off += w < wave ? wcnt[w] : 0u;
             tot += wcnt[w];
         }
@@ -490,25 +506,40 @@ extern "C" int pulsar_moe_route(void *selected, void *weights, void *ptrs, void 
                                 const void *logits, const void *router_bias, uint32_t n_expert, uint32_t k_used,
                                 float weight_scale, uint32_t softmax_mode, const pulsar_expert_bank *bank,
                                 const pulsar_expert_ptrs *shared, uint32_t n_shared, uint32_t n_tok) {
+    const uint32_t n_slots = k_used + n_shared;
     if (!selected || !weights || !ptrs || !slot_weights || !active || !logits || !bank || n_tok == 0 ||
         k_used == 0 || k_used > n_expert || n_expert > 64u * pk::kMaxPerLane || softmax_mode > 1u ||
-        n_shared > pk::kMaxShared || (n_shared && !shared) || k_used + n_shared > 64u ||
-        (uint64_t)n_tok * k_used > pk::kMaxCsrPairs)
+        n_shared > pk::kMaxShared || (n_shared && !shared) || n_slots > 16u ||
+        (uint64_t)n_tok * n_slots > pk::kMaxCsrPairs)
         return pk::reject("moe route");
     pk::SharedSlots sh = {};
     for (uint32_t s = 0; s < n_shared; s++) sh.p[s] = shared[s];
+    // lanes per token: as many as let the block's 16 waves route every token
+    // in one round (c4's 16 tokens: a wave each; c5's 64: 16 lanes each),
+    // at least the token's slots, and enough that J = experts per lane <= 16
+    auto pow2 = [](uint32_t v) {
+        uint32_t p = 1u;
+        while (p < v) p <<= 1;
+        return p;
+    };
+    const uint32_t tpw = pow2((n_tok + pk::kCsrThreads / 64u - 1u) / (pk::kCsrThreads / 64u));
+    uint32_t lpt = tpw >= 16u ? 4u : 64u / tpw;
+    lpt = lpt > pow2(n_slots) ? lpt : pow2(n_slots);
+    lpt = lpt > 4u ? lpt : 4u;
+    while ((n_expert + lpt - 1u) / lpt > 16u) lpt <<= 1;
+    const uint32_t jl = pow2((n_expert + lpt - 1u) / lpt);
 #define PK_RT(J)                                                                                                 \
-    hipLaunchKernelGGL(pk::route_kernel<J>, dim3(1), dim3(64u * pk::kRouteWaves), 0, pk::stream(),              \
-                       (int32_t *)selected, (float *)weights, (pulsar_expert_ptrs *)ptrs, (float *)slot_weights, \
-                       (uint32_t *)active, (const float *)logits, (const float *)router_bias, n_expert, k_used,   \
-                       weight_scale, softmax_mode, *bank, sh, n_shared, n_tok)
-    if (n_expert <= 64u)
+    hipLaunchKernelGGL(pk::route_kernel<J>, dim3(1), dim3(pk::kCsrThreads), 0, pk::stream(), (int32_t *)selected, \
+                       (float *)weights, (pulsar_expert_ptrs *)ptrs, (float *)slot_weights, (uint32_t *)active,   \
+                       (const float *)logits, (const float *)router_bias, n_expert, k_used, weight_scale,         \
+                       softmax_mode, *bank, sh, n_shared, n_tok, lpt)
+    if (jl == 1u)
         PK_RT(1);
-    else if (n_expert <= 128u)
+    else if (jl == 2u)
         PK_RT(2);
-    else if (n_expert <= 256u)
+    else if (jl == 4u)
         PK_RT(4);
-    else if (n_expert <= 512u)
+    else if (jl == 8u)
         PK_RT(8);
     else
         PK_RT(16);

@@ -32,8 +32,8 @@ def _logits(E, n_tok, mode):
 
 @pytest.mark.parametrize("E,k,n_tok,n_sh,mode,select_bias",
                          [(128, 8, 16, 0, 1, False), (32, 4, 64, 0, 1, True), (256, 8, 3, 1, 1, False),
-                          (300, 6, 40, 2, 0, True), (12, 3, 200, 0, 1, False), (64, 20, 9, 3, 1, False),
-                          (1000, 16, 5, 0, 0, True)])
+                          (300, 6, 40, 2, 0, True), (12, 3, 200, 0, 1, False), (64, 12, 9, 3, 1, False),
+                          (1000, 16, 5, 0, 0, True), (20, 5, 70, 0, 1, False)])
 def test_route_matches_separate_calls(dev, E, k, n_tok, n_sh, mode, select_bias):
     """moe_route against router_select + moe_route_ptrs: sel, weights,
     pointers and slot weights bit-identical (ties, an all-NaN token, an
@@ -154,4 +154,6 @@ def test_experts_contract(dev):
         K.moe_down_experts(buf, buf, None, buf, bank, 4, None, 1, 2, 256, 256, L.drb, QUANT_Q6_K)
     with pytest.raises(K.KernelError):  # softmax mode 2 (sink slots) is not routed here
         K.moe_route(buf, buf, buf, buf, buf, buf, None, 4, 2, 1.0, 2, bank, None, 1)
+    with pytest.raises(K.KernelError):  # more than 16 slots
+        K.moe_route(buf, buf, buf, buf, buf, buf, None, 40, 17, 1.0, 1, bank, None, 1)
     torch.cuda.synchronize()
