@@ -693,16 +693,6 @@ PK_DEV uint32_t pk_mul16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_ushort2, a) * __builtin_bit_cast(pk_ushort2, b));
 }
 
-// Two packed int16 -> two bytes (low bytes), for the bsums split
-typedef short pk_short2 __attribute__((ext_vector_type(2)));
-PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
-    // both splits formed and one kept per lane (selects: a divergent branch
-    // here would split the hot loop into many blocks)
-    const uint32_t hx = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, x) >> (short)7);  // h = b >> 7
-    const uint32_t hy = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, y) >> (short)7);  // |h| <= 16
-    const uint32_t lx = x & 0x007f007fu, ly = y & 0x007f007fu;                                      // l = b & 127
-    return __builtin_amdgcn_perm(high ? hy : ly, high ? hx : lx, 0x06040200u);  // bytes 0, 2 of x, then of y
-}
 
 // Tiles of at most 4 pairs: the MFMA result of pairs 0..3 sits in the kq = 0
 // lanes (lane i, element r = pair r); this moves element p of lane i to lane
@@ -830,7 +820,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         if (t0 != s0) __syncthreads();  // the previous tile's activations are consumed
         if (threadIdx.x < m) pr_l[threadIdx.x] = src.pair(t0 + threadIdx.x, lst);
         __syncthreads();
-        stage_q8_rows<2>(acts_lds, m, k_blocks, act_bytes, [&](uint32_t j) {
+        stage_q8_rows<2, Q == PULSAR_QUANT_Q2_K>(acts_lds, m, k_blocks, act_bytes, [&](uint32_t j) {
             const uint32_t pr = pr_l[j];
             return act + (PAIR ? (uint64_t)(pr >> 4) : (uint64_t)(pr >> 4) * n_used + (pr & 15u)) * k_blocks;
         });
@@ -859,6 +849,8 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // their pair stages occupancy (Q4_K 127 -> 169 VGPRs)
         constexpr bool kSmallPath = Q == PULSAR_QUANT_Q2_K || kIq2 || kMx;
         const bool small = kSmallPath && m <= 4u;
+        // Q2_K tiles of one pair (most c4 groups): no gather at all
+        const bool one = Q == PULSAR_QUANT_Q2_K && m == 1u;
         float acc[NM][4], acs[NM];
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; mt++) {
@@ -1044,20 +1036,24 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                         isum[mt] = mfma16x16x32(a, b, isum[mt]);
                     }
                 }
-                // lane (pair i, kq): l (kq < 2) or h (kq >= 2) bytes of bsums 8 (kq & 1) + [0, 8)
-                const uint4 bs = *(const uint4 *)(rec + 272u + 16u * (kq & 1u));
-                const uint2 alh = make_uint2(bsum_bytes(bs.x, bs.y, kq >= 2u), bsum_bytes(bs.z, bs.w, kq >= 2u));
+                // lane (pair i, kq): the l (kq < 2) or h (kq >= 2) bytes of bsums
+                // 8 (kq & 1) + [0, 8), split when the tile was staged; zeros in
+                // the other lane groups of each operand
+                const uint2 ab = *(const uint2 *)(rec + 272u + 16u * (kq & 1u) + 8u * (kq >> 1));
+                const uint2 zero = make_uint2(0u, 0u);
+                const uint2 al = kq < 2u ? ab : zero, ah = kq < 2u ? zero : ab;
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
-                    // mins of sub-blocks 8 (kq & 1) + [0, 8) against l (kq < 2) and h (kq >= 2)
+                    // mins of sub-blocks 8 (kq & 1) + [0, 8)
                     const uint2 s8 = (kq & 1u) ? make_uint2(sc[mt].z, sc[mt].w) : make_uint2(sc[mt].x, sc[mt].y);
                     const uint2 mn = make_uint2((s8.x >> 4) & 0x0f0f0f0fu, (s8.y >> 4) & 0x0f0f0f0fu);
-                    const uint2 zero = make_uint2(0u, 0u);
-                    const v4i dl = mfma16x16x32(alh, kq < 2u ? mn : zero);
-                    const v4i dh = mfma16x16x32(alh, kq < 2u ? zero : mn);
+                    const v4i dl = mfma16x16x32(al, mn);
+                    const v4i dh = mfma16x16x32(ah, mn);
                     const uint32_t dd = *(const uint32_t *)(ws + mt * 16u * kRowL + tail_at);
                     const float xd = f16f((uint16_t)dd), xmin = f16f((uint16_t)(dd >> 16));
-                    if (small) {
+                    if (one) {  // a single pair: its values are element 0 of the kq = 0 lanes already
+                        acs[mt] += yd1 * xd * (float)isum[mt][0] - yd1 * xmin * (float)(dl[0] + 128 * dh[0]);
+                    } else if (small) {
                         const v4i sm = {dl[0] + 128 * dh[0], dl[1] + 128 * dh[1], dl[2] + 128 * dh[2], dl[3] + 128 * dh[3]};
                         acs[mt] += yd1 * xd * (float)gather_pairs(isum[mt]) - yd1 * xmin * (float)gather_pairs(sm);
                     } else {

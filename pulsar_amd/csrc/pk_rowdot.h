@@ -94,24 +94,39 @@ PK_DEV void load_row_acts_lds(const uint8_t *row, const RowGeom &rg, Act (&a)[UP
     }
 }
 
+// Two bsums (int16 halves of x) and two more (y) -> their low 7 bits
+// (high = false, l = b & 127) or the rest (high = true, h = b >> 7), one
+// byte each: b = 128 h + l exactly, l in [0, 128), |h| <= 16 for the sums
+// of 16 int8 the quantizer writes. Both splits are formed and one kept by
+// a select (a divergent branch here would split the caller's hot loop).
+typedef short pk_short2 __attribute__((ext_vector_type(2)));
+PK_DEV uint32_t bsum_bytes(uint32_t x, uint32_t y, bool high) {
+    const uint32_t hx = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, x) >> (short)7);  // h = b >> 7
+    const uint32_t hy = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pk_short2, y) >> (short)7);
+    const uint32_t lx = x & 0x007f007fu, ly = y & 0x007f007fu;  // l = b & 127
+    return __builtin_amdgcn_perm(high ? hy : ly, high ? hx : lx, 0x06040200u);  // bytes 0, 2 of x, then of y
+}
+
 // Block-wide copy of m q8_K rows (k_blocks blocks each) into LDS in the
 // load_act_lds layout, row j at byte j * row_pitch; row j comes from the
 // global q8_K row src_row(j).
 // A block is copied as 16 + 2 16-byte pieces (qs, bsums) and its d, all
 // loads of a batch of B per thread issued before their stores (B trades
-// registers for loads in flight).
-template <uint32_t B, typename RowFn>
+// registers for loads in flight). SPLIT: each bsums piece (8 int16) is
+// stored as the int8 bytes of its 128 h + l split instead, l bytes of the
+// 8 sums then h bytes (the operands of the grouped Q2_K min-term MFMAs).
+template <uint32_t B, bool SPLIT = false, typename RowFn>
 PK_DEV void stage_q8_rows(uint8_t *lds, uint32_t m, uint32_t k_blocks, uint32_t row_pitch, RowFn src_row) {
     const uint32_t per_row = k_blocks * 19u, total = m * per_row;
     for (uint32_t base = threadIdx.x; base < total; base += B * blockDim.x) {
         uint4 v[B];
         uint32_t dst[B];
-        bool is_d[B];
+        bool is_d[B], is_bs[B];
 #pragma unroll
         for (uint32_t u = 0; u < B; u++) {
             const uint32_t it = base + u * blockDim.x;
             dst[u] = UINT32_MAX;
-            is_d[u] = false;
+            is_d[u] = is_bs[u] = false;
             if (it < total) {
                 const uint32_t j = it / per_row, r = it - j * per_row, sb = r / 19u, c = r - sb * 19u;
                 const uint8_t *src = (const uint8_t *)src_row(j) + (uint64_t)sb * 292u;
@@ -120,16 +135,22 @@ PK_DEV void stage_q8_rows(uint8_t *lds, uint32_t m, uint32_t k_blocks, uint32_t 
                 const uint32_t dofs = c < 16u ? 16u + 16u * c : c == 16u ? 272u : c == 17u ? 288u : 0u;
                 dst[u] = j * row_pitch + sb * kActLdsPitch + dofs;
                 is_d[u] = c == 18u;
+                is_bs[u] = c == 16u || c == 17u;
                 v[u] = c < 18u ? ld128(src + so) : make_uint4(ld32(src), 0u, 0u, 0u);
             }
         }
 #pragma unroll
         for (uint32_t u = 0; u < B; u++) {
             if (dst[u] == UINT32_MAX) continue;
-            if (is_d[u])
+            if (is_d[u]) {
                 *(uint32_t *)(lds + dst[u]) = v[u].x;  // d
-            else
-                *(uint4 *)(lds + dst[u]) = v[u];
+            } else {
+                uint4 x = v[u];
+                if (SPLIT && is_bs[u])
+                    x = make_uint4(bsum_bytes(v[u].x, v[u].y, false), bsum_bytes(v[u].z, v[u].w, false),
+                                   bsum_bytes(v[u].x, v[u].y, true), bsum_bytes(v[u].z, v[u].w, true));
+                *(uint4 *)(lds + dst[u]) = x;
+            }
         }
     }
 }
