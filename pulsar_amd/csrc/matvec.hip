@@ -23,8 +23,11 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
 // weight units are requested first, then (once per wave) the token's
 // activation slices, so the HBM latency of the first row overlaps the L2
 // latency of the activations.
+#ifndef PK_MV_TPB
+#define PK_MV_TPB 256u
+#endif
 template <uint32_t Q, uint32_t T, uint32_t UPLMAX, uint32_t RPW, uint32_t L2>
-__global__ __launch_bounds__(256) void matvec_kernel(float *__restrict__ out,
+__global__ __launch_bounds__(PK_MV_TPB) void matvec_kernel(float *__restrict__ out,
                                                      const uint8_t *__restrict__ w,
                                                      const pulsar_block_q8_K *__restrict__ xq,
                                                      uint32_t n_units, uint32_t nblk32,
@@ -134,13 +137,14 @@ static void launch_matvec(float *out, const uint8_t *w, const pulsar_block_q8_K 
     constexpr uint32_t kCap = Q == PULSAR_QUANT_Q6_K ? 3072u : 6144u;
     const uint32_t chunks = (n_pass + RPW - 1u) / RPW;
     const uint32_t waves = chunks <= PK_MV_WAVES ? chunks : chunks < kCap ? chunks : kCap;
-    const dim3 grid((waves + 3u) / 4u, (n_tok + T - 1u) / T);
+    constexpr uint32_t wpb = PK_MV_TPB / 64u;
+    const dim3 grid((waves + wpb - 1u) / wpb, (n_tok + T - 1u) / T);
     if (lpr_log2 == 6)
-        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 6>), grid, dim3(256), 0, pk::stream(), out, w, xq,
-                           n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
+        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 6>), grid, dim3(PK_MV_TPB), 0, pk::stream(), out, w,
+                           xq, n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
     else
-        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 0>), grid, dim3(256), 0, pk::stream(), out, w, xq,
-                           n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
+        hipLaunchKernelGGL((matvec_kernel<Q, T, UPLMAX, RPW, 0>), grid, dim3(PK_MV_TPB), 0, pk::stream(), out, w,
+                           xq, n_units, nblk32, lpr_log2, in_blocks, out_dim, n_tok, row_bytes, n_pass);
 }
 
 

@@ -157,3 +157,44 @@ def test_experts_contract(dev):
     with pytest.raises(K.KernelError):  # more than 16 slots
         K.moe_route(buf, buf, buf, buf, buf, buf, None, 40, 17, 1.0, 1, bank, None, 1)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dq,ffn", [(QUANT_Q6_K, 2048), (QUANT_IQ2_XXS, 2048), (QUANT_MXFP4, 2880)],
+                         ids=["q6k", "iq2xxs", "mxfp4"])
+def test_grouped_fma_epilogue_error_bound(dev, dq, ffn):
+    """The grouped stages of the single-product formats fold each super-block
+    value into the row sum with one fused multiply-add (one rounding, where
+    the CPU lane rounds the product, then the sum); the super-blocks are
+    added in the lane's order. So every partial row stays within one f32
+    rounding of the running magnitude per super-block step of the lane's
+    value: |delta| <= n_steps * 2^-23 * sum_b |f_b|, n_steps the row's
+    super-blocks (MXFP4: its 32-value blocks too). Checked on every routed
+    pair's down row against the oracle's row dots."""
+    import oracle
+
+    hidden, E, k, n_tok = 512, 12, 4, 9
+    L = Layer(QUANT_Q4_K, dq, hidden=hidden, ffn=ffn, E=E, n_used=k, n_tok=1)
+    bank = _bank(L)
+    logits = torch.from_numpy(rng.standard_normal((n_tok, E)).astype(np.float32)).to(dev)
+    u8 = dict(dtype=torch.uint8, device=dev)
+    sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
+    rw = torch.zeros((n_tok, k), dtype=torch.float32, device=dev)
+    ptrs = torch.zeros(n_tok * k * 48, **u8)
+    slot_w = torch.zeros((n_tok, k), dtype=torch.float32, device=dev)
+    active = torch.zeros(2 + E, dtype=torch.int32, device=dev)
+    K.moe_route(sel, rw, ptrs, slot_w, active, logits, None, E, k, 1.0, 1, bank, None, n_tok)
+    mids = (rng.standard_normal((n_tok * k, ffn)) * 0.05).astype(np.float32)
+    midq = oracle.quantize_q8_k(mids)
+    partial = torch.full((n_tok * k, hidden), float("nan"), dtype=torch.float32, device=dev)
+    K.moe_down_experts(partial, sel, active, torch.from_numpy(midq.reshape(-1)).to(dev), bank, E, None, n_tok, k,
+                       ffn, hidden, L.drb, dq)
+    torch.cuda.synchronize()
+    got = down(partial)
+    ids = down(sel).reshape(-1)
+    n_steps = -(-ffn // 256) + (ffn // 32 if dq == QUANT_MXFP4 else 0)
+    worst = 0.0
+    for so, e in enumerate(ids):
+        want, scale = oracle.rows_dot(L.d[e], L.drb, hidden, midq[so:so + 1], ffn, 1, dq, 4)
+        ratio = np.abs(got[so] - want[0]) / np.maximum(scale[0], 1e-30)
+        worst = max(worst, float(ratio.max()))
+    assert worst <= n_steps * 2.0 ** -23, (worst, n_steps)

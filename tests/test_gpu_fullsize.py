@@ -1,7 +1,8 @@
 """Parity at the benchmark configurations' full shapes, against the oracle.
 
 Dense matvec (pulsar_matmul_kq): config 1 (Q4_K 4096x4096) and config 2
-(Q6_K 8192x4096) at decode batch 1 and as a 16-token chunk, matrices whose
+(Q6_K 8192x4096) at decode batch 1 and as a 16-token chunk, Q5_K and NVFP4
+chunks of 5-31 tokens over 8192 rows and more, matrices whose
 row passes exceed the decode kernel's wave grid (Q6_K 32768 rows over 3072
 waves, Q4_K / Q2_K / IQ2_XXS 16384 rows over 6144), the MFMA chunk kernel's
 32-row tiles at 8 tokens, a 64-token prefill tile, and a Q6_K lm-head of
@@ -63,6 +64,15 @@ DENSE_FULL = [
     # Q4_K at 8192 rows and more: 32-row tiles, 8-super-block chunks, 16 waves
     ("q4k_8192x4096_t16", QUANT_Q4_K, 8192, 4096, 16),
     ("q4k_14336x4096_t31", QUANT_Q4_K, 14336, 4096, 31),
+    # Q5_K and NVFP4 at 8192 rows and more: the 32-row tiles with two chunks
+    # in flight that Q6_K takes (the Q5_K fifth bits and the NVFP4 sub-block
+    # scales decoded under the prefetch), ragged K included
+    ("q5k_8192x4096_t16", fm.QUANT_Q5_K, 8192, 4096, 16),
+    ("q5k_8192x2816_t16_ragged_k", fm.QUANT_Q5_K, 8192, 2816, 16),
+    ("q5k_12288x4096_t5", fm.QUANT_Q5_K, 12288, 4096, 5),
+    ("nvfp4_8192x4096_t16", fm.QUANT_NVFP4, 8192, 4096, 16),
+    ("nvfp4_8192x2816_t7_ragged_k", fm.QUANT_NVFP4, 8192, 2816, 7),
+    ("nvfp4_8192x4096_t31", fm.QUANT_NVFP4, 8192, 4096, 31),
 ]
 
 
@@ -71,7 +81,7 @@ def _unit_scales(quant, w):
     8.0, so 0.125 * d = 1)."""
     bb = fm.BLOCK_LAYOUT[quant][1]
     blk = w.reshape(w.shape[0], -1, bb)
-    d_off, m_off, d_val = {QUANT_Q4_K: (0, 2, 0x3C00), QUANT_Q2_K: (80, 82, 0x3C00),
+    d_off, m_off, d_val = {QUANT_Q4_K: (0, 2, 0x3C00), fm.QUANT_Q5_K: (0, 2, 0x3C00), QUANT_Q2_K: (80, 82, 0x3C00),
                            QUANT_Q6_K: (208, None, 0x3C00), QUANT_IQ2_XXS: (0, None, 0x4800)}[quant]
     blk[..., d_off], blk[..., d_off + 1] = d_val & 0xFF, d_val >> 8
     if m_off is not None:
@@ -106,6 +116,8 @@ def test_dense_full_shape(dev, name, quant, rows, cols, n_tok):
     st = parity_stats(got, want, scale)
     record_parity(name, st)
     assert st["max_rel_sum_abs"] <= TOL_REL, st
+    if quant == fm.QUANT_NVFP4:
+        return  # per-sub-block float scales: no exact-integer form
     # unit scales: every output an exact integer, bit-exact
     _unit_scales(quant, w)
     xq1 = _unit_xq(n_tok, cols, rng)
