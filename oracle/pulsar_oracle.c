@@ -1145,7 +1145,18 @@ int po_router_select(int32_t *selected, float *weights, const float *logits,
                     best = e;
                 }
             }
-            if (best == UINT32_MAX) best = 0; /* all-NaN scores */
+            if (best == UINT32_MAX) {
+                /* every score NaN: no expert compares better than the
+                 * start, so the slot keeps (UINT32_MAX as int32 = -1,
+                 * prob 0) (cu:979-1009) and routes nowhere. The reference
+                 * kernel gives this only when its warp has no padding lane
+                 * (n_expert == 32 J, cu:1068-1090); with one, the padding
+                 * lane's -inf wins and the id is n_expert, outside the
+                 * bank. Here it is -1 in both cases, as on the GPU path. */
+                sel[k] = -1;
+                w[k] = 0.0f;
+                continue;
+            }
             sel[k] = (int32_t)best;
             w[k] = prob[best];
             sum += prob[best];

@@ -360,8 +360,9 @@ def test_router_select_softmax_with_selection_bias(dev, n_expert, k, n_tok):
 def test_router_select_ties_inf_nan(dev, mode):
     """Tied scores go to the lower index; -inf and NaN logits: NaN never
     wins, and once only -inf remain the lowest index wins again (the
-    reference's removed experts are set to -inf, not dropped)."""
-    n_expert, k, n_tok = 300, 12, 4
+    reference's removed experts are set to -inf, not dropped); a token
+    whose logits are all NaN selects -1 with prob 0 in every slot."""
+    n_expert, k, n_tok = 300, 12, 5
     logits = np.full((n_tok, n_expert), 0.5, np.float32)   # all tied
     logits[1, ::7] = -np.inf
     logits[1, 3:5] = 2.0
@@ -369,12 +370,14 @@ def test_router_select_ties_inf_nan(dev, mode):
     logits[2, 10:13] = 1.0                                  # 3 finite, k = 12
     logits[3, ::3] = np.nan
     logits[3, 100] = 3.0
+    logits[4, :] = np.nan
     bias = np.zeros(n_expert, np.float32)
     sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
     w = zeros_f32((n_tok, k))
     K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.0, n_tok, mode, 0)
     want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.0, n_tok, mode, 0)
     assert np.array_equal(down(sel), want_sel)
+    assert (want_sel[4] == -1).all()
     got_w = down(w)
     assert np.array_equal(np.isnan(got_w), np.isnan(want_w))
     ok = ~np.isnan(want_w)
@@ -407,6 +410,7 @@ def test_router_select_sigmoid_edges(dev, with_bias):
     K.router_select(sel, w, up_f32(logits), up_f32(bias), n_expert, k, 1.0, n_tok, 0, 0)
     want_sel, want_w = oracle.router_select(logits, bias, n_expert, k, 1.0, n_tok, 0, 0)
     assert np.array_equal(down(sel), want_sel)
+    assert (want_sel[4] == -1).all()
     got_w = down(w)
     assert np.array_equal(np.isnan(got_w), np.isnan(want_w))
     ok = ~np.isnan(want_w)

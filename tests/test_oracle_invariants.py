@@ -337,6 +337,35 @@ def test_router_softmax_mode_with_selection_bias(n_expert, k, seed):
         assert np.abs(w[0] - wrong).max() > 1e-3
 
 
+def test_router_nan_scores_never_win():
+    """A NaN score compares neither greater nor equal (pulsar_kernels.cu:
+    922-925), so NaN experts are never selected; once the finite experts
+    are taken (their scores set to -inf) the lowest-index taken expert wins
+    again; a token whose scores are all NaN keeps the start value
+    (UINT32_MAX, prob 0) in every slot: id -1 (cu:979-1009; the reference
+    kernel's padding lanes, when it has them, would give id n_expert
+    instead, an id outside the bank). Mode 0 then divides 0 by the 6.1e-5
+    floor, mode 1 softmaxes k zeros to 1/k."""
+    n_expert, k = 8, 4
+    raw = np.zeros((3, n_expert), np.float32)
+    raw[0] = [0.5, np.nan, 0.25, np.nan, 1.0, np.nan, np.nan, np.nan]
+    raw[1] = np.nan
+    raw[2] = np.arange(n_expert, dtype=np.float32)
+    bias = np.zeros(n_expert, np.float32)
+    bias[5] = np.nan  # a NaN bias makes that expert's score NaN
+    for mode in (0, 1):
+        sel, w = oracle.router_select(raw, bias, n_expert, k, 2.0, 3, mode)
+        # finite experts 4, 0, 2 by score, then -inf ties: lowest index 0
+        assert list(sel[0]) == [4, 0, 2, 0], mode
+        assert list(sel[1]) == [-1] * k, mode
+        assert list(sel[2]) == [7, 6, 4, 3], mode  # 5 has a NaN bias
+        if mode == 0:
+            assert (w[1] == 0).all()
+        else:
+            np.testing.assert_array_equal(w[1], np.full(k, 2.0 / k, np.float32))
+        assert np.isfinite(w).all()
+
+
 def test_router_sigmoid_mode_and_ties():
     n_expert, k = 64, 8
     logits = (rng.standard_normal((3, n_expert)) * 4).astype(np.float32)
