@@ -8,8 +8,11 @@
 //     (token, slot) pairs of one expert per MFMA tile) for Q2_K, IQ2_XXS,
 //     MXFP4, Q4_K, Q5_K and Q6_K experts.
 // Every kernel produces exact int32 group sums with MFMA, applies the
-// format's integer scales in int32, forms the per-super-block fp32 value in
-// the reference's operation order and accumulates super-blocks in order.
+// format's integer scales in int32 and accumulates super-blocks in order.
+// mmq_gemm_kernel forms each super-block's fp32 value in the reference's
+// operation order (two roundings per multiply-add); the grouped kernel's
+// epilogues are fused multiply-adds (__builtin_fmaf, one rounding), which
+// differ from the reference's sums by at most one rounding per step.
 //
 // Operand layout of v_mfma_i32_16x16x32_i8 (8 int8 per lane):
 //   A[i][k]: lane i + 16 * kq, K slots of lane group kq
@@ -721,6 +724,22 @@ PK_DEV float gather_pairs(const float (&f)[4]) {
 template <uint32_t Q>
 constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 12u : 4u;
 
+// 16-row tiles per wave: a wave walks T consecutive row tiles of its expert
+// with the weight pipeline running across the tile boundaries, so the
+// block's group record, pair list and activation staging serve T times the
+// rows. Measured (stage timings, alternating libraries): MXFP4 2 in both
+// stages (c5 64 tokens: gate / up 112.3 -> 97.5 us, its 2880 rows in 8
+// blocks of 384 so the 32 experts' blocks make one round of 256 blocks,
+// one per CU; down 56.9 -> 51.9 us; 3 and 4 leave CUs idle in the down
+// stage, 64 / 81 us); IQ2_XXS down 2 (c4 60.5 -> 57.0 us); 1 for the
+// others: Q2_K down 50.2 at 1, 50.1 / 49.4 / 51.9 at 2 / 3 / 4, and two
+// tiles in the K-quant gate / up stages cost them occupancy or block
+// count (c4 Q2_K 85.3 -> 92.0 us, IQ2_XXS 104.5 -> 150.2 us).
+template <uint32_t Q, bool PAIR>
+constexpr uint32_t kGqTiles = Q == PULSAR_QUANT_MXFP4 ? 2u : (Q == PULSAR_QUANT_IQ2_XXS && !PAIR) ? 2u : 1u;
+template <uint32_t Q, bool PAIR>
+constexpr uint32_t kGqBlockRows = 16u * kGqWaves<Q> * kGqTiles<Q, PAIR>;
+
 // amdgpu_waves_per_eu(2): register allocation for at least two waves per
 // SIMD. Left to itself the compiler spends more (Q2_K pair 164 VGPRs, Q4_K
 // 240, Q5_K 286); with the bound, 152 / 161 / 231, no spills, and the c4
@@ -765,7 +784,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     src.range(grp, lst, s0, s1);
     if (s0 >= s1) return;
     if (nul) {  // unrouted slots: their rows of this block are 0
-        const uint32_t r0 = blockIdx.x * kGqWaves<Q> * 16u, nr = kGqWaves<Q> * 16u;
+        const uint32_t nr = kGqBlockRows<Q, PAIR>, r0 = blockIdx.x * nr;
         for (uint32_t it = threadIdx.x; it < (s1 - s0) * nr; it += blockDim.x) {
             const uint32_t pr = src.pair(s0 + it / nr, lst), row = r0 + it % nr;
             if (row < n_rows) out[((uint64_t)(pr >> 4) * n_used + (pr & 15u)) * n_rows + row] = 0.0f;
@@ -774,9 +793,12 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i = lane & 15u, kq = lane >> 4;
-    const uint32_t rw0 = (blockIdx.x * kGqWaves<Q> + wave) * 16u;  // the wave's first row
-    const bool active = rw0 < n_rows;                    // wave-uniform
+    constexpr uint32_t T = kGqTiles<Q, PAIR>;
+    const uint32_t rw0 = (blockIdx.x * kGqWaves<Q> + wave) * 16u * T;  // the wave's first row
+    const bool active = rw0 < n_rows;                                  // wave-uniform
     const uint32_t n_steps = (k_blocks + S - 1u) / S;
+    // the wave's row tiles that hold rows
+    const uint32_t n_tiles = !active ? 0u : (n_rows - rw0 + 15u) / 16u < T ? (n_rows - rw0 + 15u) / 16u : T;
     auto row_src = [&](uint32_t mt, uint32_t r) {
         const uint32_t gr = rw0 + r < n_rows ? rw0 + r : n_rows - 1u;
         return as_global(PAIR && mt ? w1 : w0) + (uint64_t)gr * row_bytes;
@@ -791,25 +813,38 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     // piece in the row's last unit
     const uint8_t *wsrc[kWj];
     uint32_t wlim[kWj], wdst[kWj];
+    // the piece's step-0 address in row tile `tile` (rows past the matrix
+    // clamped to its last row, whose pieces are loaded and never stored)
+    auto wsrc_at = [&](uint32_t j, uint32_t tile) {
+        const uint32_t q = lane + 64u * j, qq = q < kWp ? q : kWp - 1u;
+        const uint32_t c = qq % F::kPieces, rs = qq / F::kPieces, sl = rs % S, rm = rs / S;
+        return row_src(rm / 16u, 16u * tile + rm % 16u) + F::piece_off(sl, c, lim);
+    };
 #pragma unroll
     for (uint32_t j = 0; j < kWj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kWp ? q : kWp - 1u;
         const uint32_t c = qq % F::kPieces, rs = qq / F::kPieces, sl = rs % S, rm = rs / S;
         const uint32_t o0 = F::piece_off(sl, c, lim);
-        wsrc[j] = row_src(rm / 16u, rm % 16u) + o0;
+        wsrc[j] = wsrc_at(j, 0u);
         wlim[j] = F::piece_off(lim, c, lim) - o0;
         wdst[j] = q < kWp ? (rm * kRowL + sl * F::kSlot + 16u * c) : UINT32_MAX;
     }
     // tails (d / dmin, MXFP4 e): kTails per (matrix, row, super-block of the step)
     const uint8_t *tsrc[kTjA];
     uint32_t tlim[kTjA], tdst[kTjA];
+    auto tsrc_at = [&](uint32_t j, uint32_t tile) {
+        const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
+        const uint32_t c = qq % (F::kTails ? F::kTails : 1u), rs = qq / (F::kTails ? F::kTails : 1u);
+        const uint32_t sl = rs % S, rm = rs / S;
+        return row_src(rm / 16u, 16u * tile + rm % 16u) + F::tail_off(sl, c, lim);
+    };
 #pragma unroll
     for (uint32_t j = 0; j < kTj; j++) {
         const uint32_t q = lane + 64u * j, qq = q < kTp ? q : kTp - 1u;
         const uint32_t c = qq % (F::kTails ? F::kTails : 1u), rs = qq / (F::kTails ? F::kTails : 1u);
         const uint32_t sl = rs % S, rm = rs / S;
         const uint32_t o0 = F::tail_off(sl, c, lim);
-        tsrc[j] = row_src(rm / 16u, rm % 16u) + o0;
+        tsrc[j] = tsrc_at(j, 0u);
         tlim[j] = F::tail_off(lim, c, lim) - o0;
         tdst[j] = q < kTp ? (rm * kRowL + sl * F::kSlot + F::kTailSlot + c) : UINT32_MAX;
     }
@@ -828,7 +863,24 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         if (!active) continue;  // wave-uniform; the block's barriers above are reached
         uint4 wv[kWj];
         uint32_t tv[kTjA];
-        auto issue = [&](uint32_t step) {
+        auto issue = [&](uint32_t tile, uint32_t step) {
+            // a new row tile: the pieces' step-0 addresses move 16 rows on
+            // (the tile before it was whole), or are formed again with the
+            // rows clamped when the tile ends past the matrix (wave-uniform
+            // branches, no loads under them)
+            if (T > 1u && step == 0u && tile > 0u) {
+                if (rw0 + 16u * tile + 16u <= n_rows) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kWj; j++) wsrc[j] += 16u * row_bytes;
+#pragma unroll
+                    for (uint32_t j = 0; j < kTj; j++) tsrc[j] += 16u * row_bytes;
+                } else {
+#pragma unroll
+                    for (uint32_t j = 0; j < kWj; j++) wsrc[j] = wsrc_at(j, tile);
+#pragma unroll
+                    for (uint32_t j = 0; j < kTj; j++) tsrc[j] = tsrc_at(j, tile);
+                }
+            }
             // the step-0 address plus the step's uniform offset, held at the
             // lane's last unit of the row (units past the row are loaded
             // from it, never used): one min and one 64-bit add per load
@@ -1102,50 +1154,76 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 }
             }
         };
-        issue(0);
-        for (uint32_t step = 0; step < n_steps; step++) {
+        // lane (row i, kq) of row tile `tile`: pairs 4kq + r of the pair
+        // tile (small tiles: pair kq); the accumulators restart at zero
+        auto store_tile = [&](uint32_t tile) {
+            const uint32_t orow = rw0 + 16u * tile + i;
+            if (orow < n_rows) {
 #pragma unroll
-            for (uint32_t j = 0; j < kWj; j++)
-                if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
-#pragma unroll
-            for (uint32_t j = 0; j < kTj; j++) {
-                if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
-                if (F::kTailBytes == 4u)
-                    *(uint32_t *)(wl_w + tdst[j]) = tv[j];
-                else if (F::kTailBytes == 2u)
-                    *(uint16_t *)(wl_w + tdst[j]) = (uint16_t)tv[j];
-                else
-                    wl_w[tdst[j]] = (uint8_t)tv[j];
-            }
-            // the wave's own LDS slots: visible to the wave's other lanes
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            issue(step + 1u < n_steps ? step + 1u : n_steps - 1u);  // in flight while this step is decoded
-#pragma unroll
-            for (uint32_t sl = 0; sl < S; sl++)
-                if (step * S + sl < k_blocks) sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot);
-            // this step's LDS reads are consumed before the next copy
-            __builtin_amdgcn_wave_barrier();
-        }
-        // lane (row i, kq): pairs 4kq + r of the tile (small tiles: pair kq)
-        const uint32_t orow = rw0 + i;
-        if (orow < n_rows) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t pi = small ? kq : 4u * kq + r;
-                if (pi >= m || (small && r > 0)) break;
-                const uint32_t pr = pr_l[pi];
-                const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
-                if (PAIR) {
-                    float g = small ? acs[0] : acc[0][r], u = small ? acs[NM - 1] : acc[NM - 1][r];
-                    if (p.gate_b) g += ldwf(p.gate_b + orow);
-                    if (p.up_b) u += ldwf(p.up_b + orow);
-                    out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
-                } else {
-                    out[so * n_rows + orow] = small ? acs[0] : acc[0][r];
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t pi = small ? kq : 4u * kq + r;
+                    if (pi >= m || (small && r > 0)) break;
+                    const uint32_t pr = pr_l[pi];
+                    const uint64_t so = (uint64_t)(pr >> 4) * n_used + (pr & 15u);
+                    if (PAIR) {
+                        float g = small ? acs[0] : acc[0][r], u = small ? acs[NM - 1] : acc[NM - 1][r];
+                        if (p.gate_b) g += ldwf(p.gate_b + orow);
+                        if (p.up_b) u += ldwf(p.up_b + orow);
+                        out[so * n_rows + orow] = glu(g, u, act_op) * weights[so];
+                    } else {
+                        out[so * n_rows + orow] = small ? acs[0] : acc[0][r];
+                    }
                 }
             }
+#pragma unroll
+            for (uint32_t mt = 0; mt < NM; mt++) {
+                acs[mt] = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
+            }
+        };
+        if (T > 1u && t0 != s0) {  // a later pair tile: back to the first row tile
+#pragma unroll
+            for (uint32_t j = 0; j < kWj; j++) wsrc[j] = wsrc_at(j, 0u);
+#pragma unroll
+            for (uint32_t j = 0; j < kTj; j++) tsrc[j] = tsrc_at(j, 0u);
+        }
+        issue(0u, 0u);
+        // (tile, step) in order; the next one's loads are in flight while
+        // this one is decoded (past the last, the last again: never stored)
+        const uint32_t tiles = T == 1u ? 1u : n_tiles;
+        for (uint32_t tile = 0; tile < tiles; tile++) {
+            for (uint32_t step = 0; step < n_steps; step++) {
+#pragma unroll
+                for (uint32_t j = 0; j < kWj; j++)
+                    if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
+#pragma unroll
+                for (uint32_t j = 0; j < kTj; j++) {
+                    if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
+                    if (F::kTailBytes == 4u)
+                        *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+                    else if (F::kTailBytes == 2u)
+                        *(uint16_t *)(wl_w + tdst[j]) = (uint16_t)tv[j];
+                    else
+                        wl_w[tdst[j]] = (uint8_t)tv[j];
+                }
+                // the wave's own LDS slots: visible to the wave's other lanes
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                uint32_t nt = tile, ns = step + 1u;
+                if (ns == n_steps) {
+                    ns = tile + 1u < tiles ? 0u : step;
+                    nt = tile + 1u < tiles ? tile + 1u : tile;
+                }
+                issue(nt, ns);
+#pragma unroll
+                for (uint32_t sl = 0; sl < S; sl++)
+                    if (step * S + sl < k_blocks) sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot);
+                // this step's LDS reads are consumed before the next copy
+                __builtin_amdgcn_wave_barrier();
+            }
+            store_tile(tile);
         }
     }
 }
@@ -1175,7 +1253,7 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const G &src, c
     const size_t lds = (size_t)lst_off + lst_bytes;
 #define PK_GQ(Q, P)                                                                                              \
     hipLaunchKernelGGL((moe_grouped_mmq_kq_kernel<Q, P, G>),                                                     \
-                       dim3((n_rows + 16u * kGqWaves<Q> - 1u) / (16u * kGqWaves<Q>), n_group),                     \
+                       dim3((n_rows + kGqBlockRows<Q, P> - 1u) / kGqBlockRows<Q, P>, n_group),                     \
                        dim3(64u * kGqWaves<Q>), lds, pk::stream(), out, src, weights, act, k_blocks, lim, n_rows, \
                        n_used, row_bytes, act_op, pmax, lst_off)
     if (quant == PULSAR_QUANT_Q2_K && pair)

@@ -7,11 +7,14 @@
 //   down : one block per (row group, token); the block's 4 waves split the
 //          token's slots, each slot's row dot lands in LDS and the slots
 //          are summed in slot order.
-// Grouped path (CSR by expert, pulsar_kernels.cu:2689-2789): Q2_K, IQ2_XXS
-// and MXFP4 experts run on the int8 matrix cores (mmq.hip); Q4_K / Q6_K
-// experts here, one block per (row block, expert group): the group's pair
-// activations are staged in LDS once, and each wave streams row passes of
-// the expert, dotting each pass with every pair.
+// Grouped path (pulsar_kernels.cu:2689-2789): one block per (row block,
+// expert group). Groups come from the CSR of moe_group_csr / route_group
+// (CsrGroups) or straight from the router's selected ids and the touched-
+// expert list of pulsar_moe_route (ExpertGroups). Q2_K, IQ2_XXS, MXFP4,
+// Q4_K, Q5_K and Q6_K experts run on the int8 matrix cores (mmq.hip); the
+// other formats here: the group's pair activations are staged in LDS once,
+// and each wave streams row passes of the expert, dotting each pass with
+// every pair.
 #include "pk_rowdot.h"
 #include "pk_route.h"
 
