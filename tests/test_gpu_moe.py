@@ -297,6 +297,46 @@ def test_grouped_many_pairs_per_expert(dev, q, hidden, ffn):
     _grouped_vs_oracle(L, q)
 
 
+@pytest.mark.parametrize("q", [QUANT_Q2_K, QUANT_IQ2_XXS, QUANT_Q4_K, QUANT_MXFP4])
+def test_grouped_partial_row_tiles(dev, q):
+    """Row counts that end inside a wave's 16-row tile (and inside its
+    second row tile where a wave takes two): each row's value depends only
+    on its own weights, so the first n rows of a launch over n rows equal,
+    bit for bit, those of the launch over the whole matrix. Groups of
+    several pair tiles are included (20 tokens x 2 slots over 3 experts)."""
+    hidden, ffn = (512, 256)
+    L = Layer(q, q, hidden=hidden, ffn=ffn, E=3, n_used=2, n_tok=20, biases=q == QUANT_MXFP4, seed=11)
+    L.sel[3, 1] = -1
+    act = ACT_SWIGLU_OAI if q == QUANT_MXFP4 else ACT_SILU
+    hptrs, dptrs = L.ptrs()
+    xq = up(oracle.quantize_q8_k(L.x))
+    ids, starts, pairs = synth.csr_by_expert(L.sel, L.n_used)
+    gptrs = up(K.expert_ptrs([L.dev_entries(int(e)) for e in ids]))
+    starts, pairs, w = up(starts), up(pairs), up_f32(L.w)
+    n_pairs = L.n_tok * L.n_used
+
+    def pair(rows):
+        # NaN-filled: the CSR stage leaves the NULL slot's row alone in both launches
+        mid = torch.full((n_pairs, rows), float("nan"), dtype=torch.float32, device=dev)
+        K.moe_pair_swiglu_grouped(mid, gptrs, starts, pairs, w, xq, hidden, rows, L.n_used, len(ids), L.grb, q,
+                                  act)
+        return down(mid)
+
+    full = pair(ffn)
+    for rows in (200, 24, 8, 1):
+        assert np.array_equal(pair(rows).view(np.uint32), full[:, :rows].view(np.uint32)), rows
+    midq = up(oracle.quantize_q8_k(np.nan_to_num(full)))
+
+    def down_rows(rows):
+        part = torch.zeros((n_pairs, rows), dtype=torch.float32, device=dev)
+        K.moe_down_grouped(part, gptrs, starts, pairs, midq, ffn, rows, L.n_used, len(ids), L.drb, q)
+        return down(part)
+
+    full_d = down_rows(hidden)
+    for rows in (200, 40, 8, 1):
+        assert np.array_equal(down_rows(rows).view(np.uint32), full_d[:, :rows].view(np.uint32)), rows
+
+
 def _grouped_vs_oracle(L: Layer, q):
     act = ACT_SWIGLU_OAI if q == QUANT_MXFP4 else ACT_SILU
     hptrs, dptrs = L.ptrs()
