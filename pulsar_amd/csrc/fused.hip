@@ -264,6 +264,8 @@ struct PairRoutedLaunch {
     uint32_t j_per_lane;
     template <uint32_t Q, uint32_t U, uint32_t NPL>
     int go() {
+        if (j_per_lane == 1u) return go_j<Q, U, 1, NPL>();
+        if (j_per_lane == 2u) return go_j<Q, U, 2, NPL>();
         if (j_per_lane == 4u) return go_j<Q, U, 4, NPL>();
         if (j_per_lane == 8u) return go_j<Q, U, 8, NPL>();
         return go_j<Q, U, 16, NPL>();
@@ -283,7 +285,9 @@ struct PairRoutedLaunch {
     }
     template <uint32_t Q, uint32_t U>
     int run() {
-        j_per_lane = n_expert <= 256u ? 4u : n_expert <= 512u ? 8u : 16u;
+        // experts per lane of the top-k: the fewest that hold them all (a
+        // lane's best is a scan over its J entries in every round)
+        j_per_lane = n_expert <= 64u ? 1u : n_expert <= 128u ? 2u : n_expert <= 256u ? 4u : n_expert <= 512u ? 8u : 16u;
         return with_stage<Q, U>(g, *this);
     }
 };

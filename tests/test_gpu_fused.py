@@ -29,6 +29,10 @@ CASES = [
     (fm.QUANT_IQ1_S, fm.QUANT_NVFP4, 512, 512, 12, 3, 3, 0, 0, ACT_SILU, False, True, True),
     (fm.QUANT_Q8_0, fm.QUANT_Q3_K, 768, 256, 10, 2, 2, 0, 1, ACT_SWIGLU_OAI, True, False, False),
     (fm.QUANT_IQ3_S, fm.QUANT_IQ2_S, 256, 512, 8, 4, 1, 1, 1, ACT_SILU, False, False, False),
+    # two experts per top-k lane (65..128 experts) and exactly one (64)
+    (QUANT_Q4_K, QUANT_Q6_K, 256, 256, 100, 8, 2, 0, 1, ACT_SILU, False, False, True),
+    (QUANT_MXFP4, QUANT_MXFP4, 320, 256, 128, 4, 3, 1, 1, ACT_SWIGLU_OAI, True, True, False),
+    (QUANT_Q2_K, QUANT_Q2_K, 256, 256, 65, 6, 2, 0, 0, ACT_SILU, False, False, True),
     # the c5 batch-1 shape (MXFP4 rows staged through LDS)
     (QUANT_MXFP4, QUANT_MXFP4, 2880, 2880, 6, 4, 1, 0, 1, ACT_SWIGLU_OAI, True, True, False),
 ]
