@@ -140,7 +140,13 @@ extern "C" int pulsar_router_select(void *selected, void *weights, const void *l
     hipLaunchKernelGGL(pk::router_select_kernel<J>, dim3(n_tok), dim3(64), 0, pk::stream(), (int32_t *)selected, \
                        (float *)weights, (const float *)logits, (const float *)bias, n_expert, k_used,           \
                        weight_scale, softmax_mode, n_shexp)
-    if (n_expert <= 256u)
+    // the fewest experts per lane that hold them all (a lane's best is a
+    // scan over its J entries in every round)
+    if (n_expert <= 64u)
+        PK_SELECT(1);
+    else if (n_expert <= 128u)
+        PK_SELECT(2);
+    else if (n_expert <= 256u)
         PK_SELECT(4);
     else if (n_expert <= 512u)
         PK_SELECT(8);

@@ -416,19 +416,20 @@ def test_router_select_softmax_with_selection_bias(dev, n_expert, k, n_tok):
 
 
 @pytest.mark.parametrize("mode", [0, 1])
-def test_router_select_ties_inf_nan(dev, mode):
+@pytest.mark.parametrize("n_expert", [300, 120, 64])
+def test_router_select_ties_inf_nan(dev, mode, n_expert):
     """Tied scores go to the lower index; -inf and NaN logits: NaN never
     wins, and once only -inf remain the lowest index wins again (the
     reference's removed experts are set to -inf, not dropped); a token
     whose logits are all NaN selects -1 with prob 0 in every slot."""
-    n_expert, k, n_tok = 300, 12, 5
+    k, n_tok = 12, 5
     logits = np.full((n_tok, n_expert), 0.5, np.float32)   # all tied
     logits[1, ::7] = -np.inf
     logits[1, 3:5] = 2.0
     logits[2, :] = -np.inf
     logits[2, 10:13] = 1.0                                  # 3 finite, k = 12
     logits[3, ::3] = np.nan
-    logits[3, 100] = 3.0
+    logits[3, min(100, n_expert - 1)] = 3.0
     logits[4, :] = np.nan
     bias = np.zeros(n_expert, np.float32)
     sel = torch.zeros((n_tok, k), dtype=torch.int32, device=dev)
