@@ -31,7 +31,9 @@ token batch. Timing: HIP events on the per-thread default stream (the stream
 every pulsar_* launch uses) around the steps, eagerly and as HIP-graph
 replays captured on that stream (the reference decodes from CUDA graphs,
 crates/kernels/src/lib.rs:755-811); the reported figure is the median of
-five timed replays, each of the same K steps between synchronizations.
+five timed replays, each of the same K steps between synchronizations,
+after the graph has been replayed untimed for 50 ms (the first replays after
+a pause run 4-8% slower while the GPU's clocks ramp up).
 
 cpu_baseline: the oracle's C restatement of the reference CPU lane
 (oracle/pulsar_oracle.c, AVX2 dots bit-identical to the scalar ones, the
@@ -87,9 +89,11 @@ class Timer:
     on that stream as the reference's decode graphs are
     (crates/kernels/src/lib.rs:755-811). The graph figure is the median of
     REPLAYS timed replays, each of exactly n steps between synchronizations
-    (one replay of a ~3 ms layer chain moved by up to 5% from run to run)."""
+    (one replay of a ~3 ms layer chain moved by up to 5% from run to run),
+    after untimed replays of the same graph for WARM_S seconds."""
 
     REPLAYS = 5
+    WARM_S = 0.05
 
     def __init__(self, torch, K):
         from pulsar_amd import runtime
@@ -109,8 +113,15 @@ class Timer:
         e1.synchronize()
         eager = e0.elapsed_ms(e1) / steps
         g = rt.Graph.capture(lambda: [step(warmup + i) for i in range(steps)])
-        g.launch()  # warm replay
-        rt.sync()
+        # untimed replays for WARM_S of GPU work first: after a pause the
+        # first replays run 4-8% slower and level off after ~25 ms (the
+        # clocks ramping up), which the timed replays should not carry
+        t_warm = time.perf_counter()
+        while True:
+            g.launch()
+            rt.sync()
+            if time.perf_counter() - t_warm >= self.WARM_S:
+                break
         times = []
         for _ in range(self.REPLAYS):
             e0.record()
