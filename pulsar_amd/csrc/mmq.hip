@@ -901,8 +901,12 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // their pair stages occupancy (Q4_K 127 -> 169 VGPRs)
         constexpr bool kSmallPath = Q == PULSAR_QUANT_Q2_K || kIq2 || kMx;
         const bool small = kSmallPath && m <= 4u;
-        // Q2_K tiles of one pair (most c4 groups): no gather at all
-        const bool one = Q == PULSAR_QUANT_Q2_K && m == 1u;
+        // tiles of one pair (most c4 groups): its values are element 0 of
+        // the kq = 0 lanes, so no gather, and the IQ2_XXS gate / up stage
+        // forms its per-element scale products for that element only (c4
+        // 97.9 -> 96.4 us; in the down stage the second copy of the group
+        // loop cost a wave per SIMD, 54.7 -> 55.4 us)
+        const bool one = (Q == PULSAR_QUANT_Q2_K || (kIq2 && PAIR)) && m == 1u;
         float acc[NM][4], acs[NM];
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; mt++) {
@@ -953,7 +957,6 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                         const uint2 qq = *(const uint2 *)(ws + mt * 16u * kRowL + 16u * bl + 8u * (kq >> 1));
                         const v4i d = mfma16x16x32(a, make_uint2(mxfp4_kv4(qq.x >> nsh), mxfp4_kv4(qq.y >> nsh)));
                         const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
-#pragma unroll
                         for (int r = 0; r < 4; r++) f[mt][r] = __builtin_fmaf(sc, (float)d[r], f[mt][r]);
                     }
                 }
@@ -1127,24 +1130,42 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
 #ifndef PK_GQ_IQ2_UNROLL
 #define PK_GQ_IQ2_UNROLL 2
 #endif
+                // the group loop in two copies (a single-pair tile scales one
+                // element), chosen once per super-block
+                auto groups = [&](auto one_c) {
 #pragma unroll PK_GQ_IQ2_UNROLL
-                for (uint32_t g = 0; g < 8; g++) {
-                    const uint2 a = a_at(g);
+                    for (uint32_t g = 0; g < 8; g++) {
+                        const uint2 a = a_at(g);
 #pragma unroll
-                    for (uint32_t mt = 0; mt < NM; mt++) {
-                        const uint2 aux = *(const uint2 *)(ws + mt * 16u * kRowL + 8u * g);
-                        uint2 b;
-                        iq2_signed8(lut, (aux.x >> (8u * kq)) & 0xffu, (aux.y >> (7u * kq)) & 127u, b.x, b.y);
-                        const v4i d = mfma16x16x32(a, b);
-                        const int32_t ls = (int32_t)(2u * (aux.y >> 28) + 1u);
+                        for (uint32_t mt = 0; mt < NM; mt++) {
+                            const uint2 aux = *(const uint2 *)(ws + mt * 16u * kRowL + 8u * g);
+                            uint2 b;
+                            iq2_signed8(lut, (aux.x >> (8u * kq)) & 0xffu, (aux.y >> (7u * kq)) & 127u, b.x, b.y);
+                            const v4i d = mfma16x16x32(a, b);
+                            const int32_t ls = (int32_t)(2u * (aux.y >> 28) + 1u);
+                            if constexpr (decltype(one_c)::value) {
+                                bsum[mt][0] += __mul24(d[0], ls);
+                            } else {
 #pragma unroll
-                        for (int r = 0; r < 4; r++) bsum[mt][r] += __mul24(d[r], ls);
+                                for (int r = 0; r < 4; r++) bsum[mt][r] += __mul24(d[r], ls);
+                            }
+                        }
                     }
+                };
+                if constexpr (PAIR) {
+                    if (one)
+                        groups(std::true_type{});
+                    else
+                        groups(std::false_type{});
+                } else {
+                    groups(std::false_type{});
                 }
 #pragma unroll
                 for (uint32_t mt = 0; mt < NM; mt++) {
                     const float xd8 = 0.125f * f16f(*(const uint16_t *)(ws + mt * 16u * kRowL + F::kTailSlot));
-                    if (small) {
+                    if (one) {
+                        acs[mt] = __builtin_fmaf(xd8 * yd1, (float)bsum[mt][0], acs[mt]);
+                    } else if (small) {
                         const v4i bs = {bsum[mt][0], bsum[mt][1], bsum[mt][2], bsum[mt][3]};
                         acs[mt] = __builtin_fmaf(xd8 * yd1, (float)gather_pairs(bs), acs[mt]);
                     } else {
