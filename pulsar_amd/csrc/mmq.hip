@@ -570,8 +570,9 @@ int launch_gemm(uint32_t quant, float *out, const uint8_t *w, const pulsar_block
 // Q2_K (84 B: scales[16] @0, qs[64] @16, f16 d, dmin @80): value
 // 32t + 8kq + i sits in qs byte 32(t / 4) + 16(kq / 2) + 8(kq % 2) + i at
 // bits 2(t % 4), sub-block 2t + kq / 2. Codes are pre-scaled by their
-// sub-block scale (3 x 15 fits int8: v_perm_b32 picks from the bytes
-// {0, sc, 2sc, 3sc}), so the 8 chained MFMAs of a super-block give
+// sub-block scale (3 x 15 fits int8; one v_pk_mul_lo_u16 scales four code
+// bytes, two per 16-bit half, c sc <= 45 so no carry crosses a byte), so
+// the 8 chained MFMAs of a super-block give
 // isum = sum_c (sc_c & 15) sum q q8 exactly; summs = sum_c bsums_c
 // (sc_c >> 4) comes from two MFMAs on bsums split as 128 h + l, l in
 // [0, 128). Super-block value yd xd isum - yd xmin summs (cpu_dot.rs:732-767).
@@ -685,6 +686,10 @@ struct GmmqFmt<PULSAR_QUANT_Q6_K> {
 constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy step
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
+#ifndef PK_GQ_ACT_LDS_PAIR
+#define PK_GQ_ACT_LDS_PAIR 24576u
+#endif
+constexpr uint32_t kGqActLdsPair = PK_GQ_ACT_LDS_PAIR;  // the same for gate / up stages (see the launch)
 #ifndef PK_GQ_ACT_LDS_MX
 #define PK_GQ_ACT_LDS_MX 61440u
 #endif
@@ -1266,7 +1271,15 @@ int launch_grouped_mmq_kq(bool pair, uint32_t quant, float *out, const G &src, c
     const uint32_t per_pair = act_row_pitch(k_blocks);
     // MXFP4 layers route many pairs to each expert (gpt-oss: 64 tokens x 4 of
     // 32 experts), so their tiles take more pairs per weight pass
-    const uint32_t budget = quant == PULSAR_QUANT_MXFP4 ? kGqActLdsMx : kGqActLds;
+    // Gate / up tiles of 4096-value rows hold 5 pairs instead of 3 (4880 bytes
+    // each), so an expert with 4 or 5 pairs takes one weight pass, not two;
+    // their blocks keep 3 per CU (VGPRs allow no more; Q2_K: 26.7 KiB static
+    // + 24.4 KiB tile + the pair list, x 3 < 160 KiB). Down stages keep 16 KiB:
+    // their blocks are smaller and 5 fit per CU. Large pair lists (many
+    // tokens) keep the smaller tile.
+    const uint32_t budget = quant == PULSAR_QUANT_MXFP4          ? kGqActLdsMx
+                            : pair && lst_bytes <= 1024u ? kGqActLdsPair
+                                                         : kGqActLds;
     if (per_pair > budget) return -1;  // one pair's row does not fit: lane kernels
     uint32_t pmax = budget / per_pair;
     pmax = pmax < kGqPairs ? pmax : kGqPairs;
