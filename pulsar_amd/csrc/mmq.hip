@@ -763,7 +763,11 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     constexpr bool kMx = Q == PULSAR_QUANT_MXFP4;
     // MXFP4, Q4_K and Q6_K super-block rows are 136-210 contiguous bytes already
     constexpr uint32_t S = (kMx || Q == PULSAR_QUANT_Q4_K || Q == PULSAR_QUANT_Q5_K || Q == PULSAR_QUANT_Q6_K) ? 1u : kGqSbs;
-    constexpr uint32_t kRowL = S * F::kSlot + 16u;        // LDS bytes per row (S slots, padded)
+    // LDS bytes per row: S slots, padded by 16 bytes (the K-quants; without
+    // the pad the c4 Q2_K gate / up stage went 81.9 -> 87.4 us, with 32
+    // bytes 83.1 us) or not at all (MXFP4: c5 64-token gate / up 96.2 ->
+    // 95.4 us, 32 bytes 95.1 us, 48 bytes 103 us)
+    constexpr uint32_t kRowL = S * F::kSlot + (kMx ? 0u : 16u);
     constexpr uint32_t kWp = NM * 16u * S * F::kPieces;  // weight pieces per step
     constexpr uint32_t kWj = (kWp + 63u) / 64u;         // ... per lane
     constexpr uint32_t kTp = NM * 16u * S * F::kTails;  // tails per step
