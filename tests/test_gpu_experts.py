@@ -72,6 +72,79 @@ def test_route_matches_separate_calls(dev, E, k, n_tok, n_sh, mode, select_bias)
     assert list(act[2:2 + len(ids)]) == ids
 
 
+def _edge_logits(E, seed):
+    """Rows that stress a top-k's order and ties: ties across the k-th
+    place, fewer non-NaN (or non--inf) scores than slots, +-inf, +-0, an
+    all-NaN row, an all--inf row, duplicates of the maximum."""
+    r = np.random.default_rng(seed)
+    rows = []
+    rows.append(np.full(E, 0.5))                                     # all equal
+    rows.append(r.integers(0, 3, E) / 2.0)                            # three values: ties straddle place k
+    x = np.full(E, np.nan); x[r.choice(E, min(3, E), replace=False)] = r.standard_normal(min(3, E))
+    rows.append(x)                                                    # three scores, the rest NaN
+    x = np.full(E, np.nan); x[r.choice(E, min(5, E), replace=False)] = [-np.inf, 1.0, -np.inf, 2.0, 0.0][:min(5, E)]
+    rows.append(x)                                                    # NaN, -inf and a few scores
+    x = np.full(E, -np.inf); x[r.choice(E, min(2, E), replace=False)] = [3.0, -1.0][:min(2, E)]
+    rows.append(x)                                                    # two scores above -inf
+    x = r.standard_normal(E); x[r.choice(E, min(4, E), replace=False)] = np.inf
+    rows.append(x)                                                    # several +inf
+    rows.append(r.choice([0.0, -0.0, 1e-30, -1e-30], E))              # signed zeros and tiny values
+    rows.append(np.full(E, np.nan))                                   # every score NaN
+    rows.append(np.full(E, -np.inf))                                  # every score -inf
+    x = r.standard_normal(E); x[r.choice(E, min(6, E), replace=False)] = x.max()
+    rows.append(x)                                                    # the maximum six times
+    x = np.full(E, np.nan); x[E - 1] = 0.25
+    rows.append(x)                                                    # one score, at the last index
+    rows.append(r.standard_normal(E))
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("E,k,mode,select_bias",
+                         [(32, 4, 1, False), (50, 8, 0, True), (100, 8, 1, False), (128, 16, 0, False),
+                          (256, 8, 1, True), (256, 1, 0, False), (500, 12, 1, False), (1000, 16, 1, True),
+                          (64, 64, 1, False), (256, 64, 0, True)])
+def test_route_topk_edges(dev, E, k, mode, select_bias):
+    """The routing of moe_route (a token per wave) and of moe_pair_routed
+    (the fused decode pair stage) against router_select's round-by-round
+    top-k, bit for bit, on rows built to stress the selection order."""
+    L = Layer(QUANT_Q4_K, QUANT_Q4_K, hidden=256, ffn=256, E=E, n_used=k, n_tok=1)
+    bank = _bank(L)
+    f32 = dict(dtype=torch.float32, device=dev)
+    lg_h = _edge_logits(E, E * 131 + k)
+    n_tok = lg_h.shape[0]
+    logits = torch.from_numpy(lg_h).to(dev)
+    sb = torch.from_numpy((np.random.default_rng(E).standard_normal(E) * 0.1).astype(np.float32)).to(dev) \
+        if select_bias else None
+
+    def bufs():
+        return dict(sel=torch.zeros((n_tok, k), dtype=torch.int32, device=dev), rw=torch.zeros((n_tok, k), **f32),
+                    ptrs=torch.zeros(n_tok * k * 48, dtype=torch.uint8, device=dev),
+                    slot_w=torch.zeros((n_tok, k), **f32))
+
+    a = bufs()
+    K.router_select(a["sel"], a["rw"], logits, sb if sb is not None else torch.zeros(E, **f32), E, k, 1.25, n_tok,
+                    mode, 0)
+    K.moe_route_ptrs(a["ptrs"], a["slot_w"], a["sel"], a["rw"], bank, E, [], n_tok, k)
+    outs = []
+    if k <= 16:  # moe_route's slot limit
+        b = bufs()
+        active = torch.zeros((2 + E,), dtype=torch.int32, device=dev)
+        K.moe_route(b["sel"], b["rw"], b["ptrs"], b["slot_w"], active, logits, sb, E, k, 1.25, mode, bank, [],
+                    n_tok)
+        outs.append(("moe_route", b))
+    c = bufs()
+    xq = torch.zeros(n_tok * q8k_blocks(256) * 292, dtype=torch.uint8, device=dev)
+    K.quantize_q8_k(xq, torch.from_numpy(L.x.repeat(n_tok, 0)).to(dev), 256, n_tok)
+    mid = torch.zeros((n_tok * k, 256), **f32)
+    K.moe_pair_routed(mid, c["ptrs"], c["slot_w"], c["sel"], c["rw"], logits, sb, E, k, 1.25, mode, bank, [], xq,
+                      256, 256, n_tok, L.grb, QUANT_Q4_K, ACT_SILU)
+    outs.append(("moe_pair_routed", c))
+    torch.cuda.synchronize()
+    for who, b in outs:
+        for name in a:
+            assert np.array_equal(down(a[name]).view(np.uint8), down(b[name]).view(np.uint8)), (who, name)
+
+
 CASES = [
     # gq, dq, hidden, ffn, E, k, n_tok, n_sh, mode, act, biases
     (QUANT_Q2_K, QUANT_Q2_K, 1024, 512, 64, 8, 16, 0, 1, ACT_SILU, False),
