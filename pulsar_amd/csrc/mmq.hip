@@ -683,6 +683,9 @@ struct GmmqFmt<PULSAR_QUANT_Q6_K> {
 #ifndef PK_GQ_ACT_LDS
 #define PK_GQ_ACT_LDS 16384u
 #endif
+#ifndef PK_GQ_MODES
+#define PK_GQ_MODES 1
+#endif
 constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy step
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
@@ -909,13 +912,23 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // acc. Q4_K, Q5_K and Q6_K keep the one path: the second one costs
         // their pair stages occupancy (Q4_K 127 -> 169 VGPRs)
         constexpr bool kSmallPath = Q == PULSAR_QUANT_Q2_K || kIq2 || kMx;
-        const bool small = kSmallPath && m <= 4u;
+        const bool small_rt = kSmallPath && m <= 4u;
         // tiles of one pair (most c4 groups): its values are element 0 of
         // the kq = 0 lanes, so no gather, and the IQ2_XXS gate / up stage
         // forms its per-element scale products for that element only (c4
         // 97.9 -> 96.4 us; in the down stage the second copy of the group
         // loop cost a wave per SIMD, 54.7 -> 55.4 us)
-        const bool one = (Q == PULSAR_QUANT_Q2_K || (kIq2 && PAIR)) && m == 1u;
+        const bool one_rt = (Q == PULSAR_QUANT_Q2_K || (kIq2 && PAIR)) && m == 1u;
+        // Q2_K walks its steps in three copies, one per epilogue (one pair,
+        // tiles of at most 4, larger), chosen once per pair tile: with the
+        // choice made per super-block, the branches' merges cost the step
+        // register copies. MODE 0: chosen at run time (the other formats).
+        using Mode0 = std::integral_constant<int, 0>;
+        auto flags = [&](auto mode_c, bool &one, bool &small) {
+            constexpr int MODE = decltype(mode_c)::value;
+            one = MODE == 0 ? one_rt : MODE == 1;
+            small = MODE == 0 ? small_rt : MODE != 3;
+        };
         float acc[NM][4], acs[NM];
 #pragma unroll
         for (uint32_t mt = 0; mt < NM; mt++) {
@@ -924,7 +937,9 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             for (int r = 0; r < 4; r++) acc[mt][r] = 0.0f;
         }
         // super-block sb from the wave's LDS slot ws (row i of matrix 0)
-        auto sb_compute = [&](uint32_t sb, const uint8_t *ws) {
+        auto sb_compute = [&](uint32_t sb, const uint8_t *ws, auto mode_c) {
+            bool one, small;
+            flags(mode_c, one, small);
             // the scales' slot offset (the row's last super-block: its copy is
             // held inside the row)
             const uint32_t tail_at = F::kTailSlot + (sb + 1u == lim ? F::kTailLast : 0u);
@@ -1186,7 +1201,10 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         };
         // lane (row i, kq) of row tile `tile`: pairs 4kq + r of the pair
         // tile (small tiles: pair kq); the accumulators restart at zero
-        auto store_tile = [&](uint32_t tile) {
+        auto store_tile = [&](uint32_t tile, auto mode_c) {
+            bool one, small;
+            flags(mode_c, one, small);
+            (void)one;
             const uint32_t orow = rw0 + 16u * tile + i;
             if (orow < n_rows) {
 #pragma unroll
@@ -1222,12 +1240,13 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // (tile, step) in order; the next one's loads are in flight while
         // this one is decoded (past the last, the last again: never stored)
         const uint32_t tiles = T == 1u ? 1u : n_tiles;
+        auto walk = [&](auto mode_c) {
         for (uint32_t tile = 0; tile < tiles; tile++) {
             for (uint32_t step = 0; step < n_steps; step++) {
-#pragma unroll
+    #pragma unroll
                 for (uint32_t j = 0; j < kWj; j++)
                     if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
-#pragma unroll
+    #pragma unroll
                 for (uint32_t j = 0; j < kTj; j++) {
                     if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
                     if (F::kTailBytes == 4u)
@@ -1249,11 +1268,56 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 issue(nt, ns);
 #pragma unroll
                 for (uint32_t sl = 0; sl < S; sl++)
-                    if (step * S + sl < k_blocks) sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot);
+                    if (step * S + sl < k_blocks)
+                        sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot, mode_c);
                 // this step's LDS reads are consumed before the next copy
                 __builtin_amdgcn_wave_barrier();
             }
-            store_tile(tile);
+            store_tile(tile, mode_c);
+        }
+        };
+        if constexpr (Q == PULSAR_QUANT_Q2_K && (PK_GQ_MODES == 2 || (PK_GQ_MODES == 1 && PAIR))) {
+            if (one_rt)
+                walk(std::integral_constant<int, 1>{});
+            else if (small_rt)
+                walk(std::integral_constant<int, 2>{});
+            else
+                walk(std::integral_constant<int, 3>{});
+        } else {  // the same walk, written out (as a lambda it compiled differently)
+        for (uint32_t tile = 0; tile < tiles; tile++) {
+            for (uint32_t step = 0; step < n_steps; step++) {
+    #pragma unroll
+                for (uint32_t j = 0; j < kWj; j++)
+                    if ((j + 1u) * 64u <= kWp || wdst[j] != UINT32_MAX) *(uint4 *)(wl_w + wdst[j]) = wv[j];
+    #pragma unroll
+                for (uint32_t j = 0; j < kTj; j++) {
+                    if ((j + 1u) * 64u > kTp && tdst[j] == UINT32_MAX) continue;
+                    if (F::kTailBytes == 4u)
+                        *(uint32_t *)(wl_w + tdst[j]) = tv[j];
+                    else if (F::kTailBytes == 2u)
+                        *(uint16_t *)(wl_w + tdst[j]) = (uint16_t)tv[j];
+                    else
+                        wl_w[tdst[j]] = (uint8_t)tv[j];
+                }
+                // the wave's own LDS slots: visible to the wave's other lanes
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                uint32_t nt = tile, ns = step + 1u;
+                if (ns == n_steps) {
+                    ns = tile + 1u < tiles ? 0u : step;
+                    nt = tile + 1u < tiles ? tile + 1u : tile;
+                }
+                issue(nt, ns);
+#pragma unroll
+                for (uint32_t sl = 0; sl < S; sl++)
+                    if (step * S + sl < k_blocks)
+                        sb_compute(step * S + sl, wl_w + i * kRowL + sl * F::kSlot, Mode0{});
+                // this step's LDS reads are consumed before the next copy
+                __builtin_amdgcn_wave_barrier();
+            }
+            store_tile(tile, Mode0{});
+        }
         }
     }
 }
