@@ -683,9 +683,6 @@ struct GmmqFmt<PULSAR_QUANT_Q6_K> {
 #ifndef PK_GQ_ACT_LDS
 #define PK_GQ_ACT_LDS 16384u
 #endif
-#ifndef PK_GQ_MODES
-#define PK_GQ_MODES 1
-#endif
 constexpr uint32_t kGqSbs = PK_GQ_SBS;         // super-blocks per row per copy step
 constexpr uint32_t kGqPairs = 16;              // pairs per tile (the MFMA's 16 columns)
 constexpr uint32_t kGqActLds = PK_GQ_ACT_LDS;  // LDS bytes for a tile's staged q8_K rows
@@ -919,10 +916,14 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // 97.9 -> 96.4 us; in the down stage the second copy of the group
         // loop cost a wave per SIMD, 54.7 -> 55.4 us)
         const bool one_rt = (Q == PULSAR_QUANT_Q2_K || (kIq2 && PAIR)) && m == 1u;
-        // Q2_K walks its steps in three copies, one per epilogue (one pair,
-        // tiles of at most 4, larger), chosen once per pair tile: with the
-        // choice made per super-block, the branches' merges cost the step
-        // register copies. MODE 0: chosen at run time (the other formats).
+        // The Q2_K and IQ2_XXS gate / up stages walk their steps in three
+        // copies, one per epilogue (one pair, tiles of at most 4, larger),
+        // chosen once per pair tile: with the choice made per super-block,
+        // the branches' merges cost every step register copies (c4 gate /
+        // up, alternating libraries: Q2_K 80.3 -> 77.7 us, IQ2_XXS 97.4 ->
+        // 92.4 us). MODE 0: chosen at run time (the other stages: the MXFP4
+        // gate / up copy spills, the Q2_K down copy costs a wave per SIMD).
+        constexpr bool kModes = (Q == PULSAR_QUANT_Q2_K || kIq2) && PAIR;
         using Mode0 = std::integral_constant<int, 0>;
         auto flags = [&](auto mode_c, bool &one, bool &small) {
             constexpr int MODE = decltype(mode_c)::value;
@@ -1276,7 +1277,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             store_tile(tile, mode_c);
         }
         };
-        if constexpr (Q == PULSAR_QUANT_Q2_K && (PK_GQ_MODES == 2 || (PK_GQ_MODES == 1 && PAIR))) {
+        if constexpr (kModes) {
             if (one_rt)
                 walk(std::integral_constant<int, 1>{});
             else if (small_rt)
