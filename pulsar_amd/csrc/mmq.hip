@@ -916,15 +916,15 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
         // 97.9 -> 96.4 us; in the down stage the second copy of the group
         // loop cost a wave per SIMD, 54.7 -> 55.4 us)
         const bool one_rt = (Q == PULSAR_QUANT_Q2_K || (kIq2 && PAIR)) && m == 1u;
-        // The Q2_K and IQ2_XXS gate / up stages (and the IQ2_XXS down
-        // stage) walk their steps in three
-        // copies, one per epilogue (one pair, tiles of at most 4, larger),
-        // chosen once per pair tile: with the choice made per super-block,
-        // the branches' merges cost every step register copies (c4 gate /
-        // up, alternating libraries: Q2_K 80.3 -> 77.7 us, IQ2_XXS 97.4 ->
-        // 92.4 us; the IQ2_XXS down stage too, 54.9 -> 53.7 us). MODE 0:
-        // chosen at run time (the other stages: the MXFP4 gate / up copy
-        // spills, the Q2_K down copy costs a wave per SIMD and time).
+        // The Q2_K gate / up stage and both IQ2_XXS stages walk their steps
+        // in three copies, one per epilogue (one pair, tiles of at most 4,
+        // larger), chosen once per pair tile: with the choice made per
+        // super-block, the branches' merges cost every step register copies
+        // (c4, alternating libraries: Q2_K gate / up 80.3 -> 77.7 us,
+        // IQ2_XXS gate / up 97.4 -> 92.4 us, IQ2_XXS down 54.9 -> 53.7 us).
+        // MODE 0: chosen at run time (the other stages: the MXFP4 gate / up
+        // copies spill, the Q2_K down copies cost a wave per SIMD and time,
+        // the MXFP4 down copies measured the same).
         constexpr bool kModes = (Q == PULSAR_QUANT_Q2_K && PAIR) || kIq2;
         using Mode0 = std::integral_constant<int, 0>;
         auto flags = [&](auto mode_c, bool &one, bool &small) {
