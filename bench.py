@@ -597,6 +597,12 @@ def cpu_baseline(seconds: float, ctx) -> dict:
 
 # --------------------------------------------------------------- PMC runs --
 
+def topk_j(n_expert: int) -> int:
+    """Experts per top-k lane of the routed pair kernel (its J template
+    argument, as pulsar_moe_pair_routed picks it)."""
+    return 1 if n_expert <= 64 else 2 if n_expert <= 128 else 4 if n_expert <= 256 else 8 if n_expert <= 512 else 16
+
+
 def pmc_run(ctx, which: str):
     """Workloads of the rocprofv3 --pmc passes: ten eager steps of each named
     configuration on rotating weights, then five copies of a 256 MiB device
@@ -658,13 +664,13 @@ def pmc_run(ctx, which: str):
         elif path == "fused_q":
             bias_d = d * s.hidden * 4 if s.biases else 0
             alg = {"pk::router_logits_q8_kernel<1u>": router + (s.n_expert * 4 if s.biases else 0),
-                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, 4u, 2u, 1u>":
+                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, {topk_j(s.n_expert)}u, 2u, 1u>":
                        gu + s.n_tok * nb_in * 292 + s.n_tok * s.n_expert * 4 + n_pairs * s.ffn * 4,
                    f"pk::moe_down_kernel<{s.down_quant}u, 1u, 2u, true>":
                        dn + bias_d + n_pairs * nb_mid * 292 + s.n_tok * s.hidden * 4}
         else:
             alg = {"pk::router_logits_q8_kernel<1u>": router,
-                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, 4u, 0u, 1u>":
+                   f"pk::moe_pair_routed_kernel<{s.gate_quant}u, 1u, {topk_j(s.n_expert)}u, 0u, 1u>":
                        gu + s.n_tok * nb_in * 292 + s.n_tok * s.n_expert * 4 + n_pairs * s.ffn * 4,
                    f"pk::moe_down_f32_kernel<{s.down_quant}u, 1u, 0u>": dn + n_pairs * s.ffn * 4 + s.n_tok * s.hidden * 4}
         print("pmc-alg " + json.dumps({"workload": name, "mean_distinct_experts": d, "alg": alg}), flush=True)
