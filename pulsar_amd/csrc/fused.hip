@@ -38,9 +38,10 @@ template <uint32_t TG>
 __global__ __launch_bounds__(256) void router_logits_q8_kernel(
         float *__restrict__ logits, pulsar_block_q8_K *__restrict__ xq, const float *__restrict__ x,
         const float *__restrict__ w, const float *__restrict__ bias, uint32_t in_dim, uint32_t n_expert,
-        uint32_t n_tok, uint32_t gemv_blocks, uint32_t nb) {
+        uint32_t n_tok, uint32_t gemv_blocks, uint32_t nb, uint32_t rb_log2) {
     if (blockIdx.x < gemv_blocks) {
-        gemv_block<TG>(logits, w, x, bias, in_dim, n_expert, n_tok, blockIdx.x);
+        gemv_block<TG>(logits, w, x, bias, in_dim, n_expert, n_tok,
+                       gemv_item(blockIdx.x, n_expert, gemv_blocks / n_expert, rb_log2));
         return;
     }
     const uint32_t gblk = (blockIdx.x - gemv_blocks) * 4u + (threadIdx.x >> 6);
@@ -348,14 +349,15 @@ extern "C" int pulsar_router_logits_q8(void *logits, void *xq, const void *x, co
     const uint64_t gemv_blocks = work;
     if (gemv_blocks + qblocks > 0x7fffffffull) return reject("router logits q8 (size)");
     const dim3 grid((uint32_t)(gemv_blocks + qblocks));
+    const uint32_t rbl = gemv_xcd_split(n_expert, (n_tok + tg - 1u) / tg, tg);
     if (tg == 1u)
         hipLaunchKernelGGL(router_logits_q8_kernel<1>, grid, dim3(256), 0, pk::stream(), (float *)logits,
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
-                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb);
+                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb, rbl);
     else
         hipLaunchKernelGGL(router_logits_q8_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)logits,
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
-                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb);
+                           in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb, rbl);
     return launch_ok("router logits q8 launch");
 }
 

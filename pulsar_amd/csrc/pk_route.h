@@ -162,6 +162,44 @@ PK_DEV void route_lane(const float *lg, const float *rbias, uint32_t n_expert, u
     e = win[0];
 }
 
+// Blocks go to the 8 XCDs round-robin (block b to XCD b % 8), each XCD with
+// its own L2. gemv_item maps block b to the item (token group * out_dim +
+// row) it computes so that the blocks of one XCD cover a band of out_dim /
+// 2^rb_log2 rows times a band of n_grp / 2^(3 - rb_log2) token groups, each
+// row and token of the band fetched into that L2 once; the host picks the
+// split that fetches the fewest bytes (rows and tokens are in_dim floats
+// each). rb_log2 = 3 is the plain order (rows interleaved over the XCDs,
+// every token group on every XCD). Only the item each block computes
+// changes, not how it computes it.
+PK_DEV uint32_t gemv_item(uint32_t b, uint32_t out_dim, uint32_t n_grp, uint32_t rb_log2) {
+    if (rb_log2 >= 3u) return b;
+    const uint32_t xcd = b & 7u, j = b >> 3;
+    const uint32_t tb_n = 8u >> rb_log2;                   // token-group bands
+    const uint32_t rows = out_dim >> rb_log2, grps = n_grp / tb_n;  // band sizes (divisible, host-checked)
+    const uint32_t rb = xcd / tb_n, tb = xcd % tb_n;
+    const uint32_t row = rb * rows + j % rows, grp = tb * grps + j / rows;
+    return grp * out_dim + row;
+}
+
+// The split gemv_item uses: rows in 2^r bands, token groups in 2^(3 - r),
+// r chosen so that an XCD fetches the fewest rows plus tokens (out_dim / 2^r
+// + n_grp tg / 2^(3 - r)); the plain order (3) on ties and where the bands
+// would not divide evenly.
+static inline uint32_t gemv_xcd_split(uint32_t out_dim, uint32_t n_grp, uint32_t tg) {
+    uint32_t best = 3u;
+    uint64_t best_cost = (uint64_t)(out_dim >> 3) + (uint64_t)n_grp * tg;
+    for (int r = 2; r >= 0; r--) {
+        const uint32_t tb = 8u >> r;
+        if (out_dim % (1u << r) != 0u || n_grp % tb != 0u) continue;
+        const uint64_t cost = (uint64_t)(out_dim >> r) + (uint64_t)(n_grp / tb) * tg;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = (uint32_t)r;
+        }
+    }
+    return out_dim % 8u == 0u || best < 3u ? best : 3u;
+}
+
 // f32 GEMV for router logits, one block of 256 threads per (row, group of
 // TG tokens): the row's K is split over the block's threads (thread i takes
 // float4 pieces i, i + 256, ... so every wave-wide load is one contiguous

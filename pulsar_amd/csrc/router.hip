@@ -11,8 +11,9 @@ namespace pk {
 template <uint32_t TG>
 __global__ __launch_bounds__(256) void matmul_f32_kernel(float *__restrict__ out, const float *__restrict__ w,
                                                          const float *__restrict__ x, uint32_t in_dim,
-                                                         uint32_t out_dim, uint32_t n_tok) {
-    gemv_block<TG>(out, w, x, nullptr, in_dim, out_dim, n_tok, blockIdx.x);
+                                                         uint32_t out_dim, uint32_t n_tok, uint32_t rb_log2) {
+    gemv_block<TG>(out, w, x, nullptr, in_dim, out_dim, n_tok,
+                   gemv_item(blockIdx.x, out_dim, gridDim.x / out_dim, rb_log2));
 }
 
 // x[r][i] += bias[i] (pulsar_kernels.cu:3621-3629)
@@ -110,12 +111,13 @@ extern "C" int pulsar_matmul_f32(void *out, const void *w, const void *x, uint32
     const uint64_t work = (uint64_t)out_dim * ((n_tok + tg - 1u) / tg);
     if (work > 0x7fffffffull) return pk::reject("matmul f32 (size)");
     const dim3 grid((uint32_t)work);
+    const uint32_t rbl = pk::gemv_xcd_split(out_dim, (n_tok + tg - 1u) / tg, tg);
     if (tg == 1u)
         hipLaunchKernelGGL(pk::matmul_f32_kernel<1>, grid, dim3(256), 0, pk::stream(), (float *)out,
-                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, rbl);
     else
         hipLaunchKernelGGL(pk::matmul_f32_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)out,
-                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok);
+                           (const float *)w, (const float *)x, in_dim, out_dim, n_tok, rbl);
     return pk::launch_ok("matmul f32 launch");
 }
 
