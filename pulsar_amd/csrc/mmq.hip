@@ -968,12 +968,17 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             const float yd1 = *(const float *)(acts_lds + (kq < m ? kq : m - 1u) * act_bytes + sb * kActLdsPitch);
             auto a_at = [&](uint32_t t) { return *(const uint2 *)(rec + 16u + 32u * t + 8u * kq); };
             if constexpr (kMx) {
-                // lane group kq: values {0, 16, 8, 24}[kq] + [0, 8) of a block,
-                // nibble kq & 1 of qs bytes 8 (kq >> 1) + [0, 8); per block the
-                // reference's sumf += scale_half(e) * sumi for sumi != 0 (an fma
-                // of a power of two and an int < 2^24 is exact, and sumi = 0
-                // adds +0 to a sum that is never -0), then yd * sumf
-                const uint32_t nsh = 4u * (kq & 1u), a_piece = (kq >> 1) + 2u * (kq & 1u);
+                // lane group kq: values 8 kq + [0, 8) of a block, nibble kq >> 1
+                // of qs bytes 8 (kq & 1) + [0, 8), so each half-wave reads 16
+                // contiguous bytes of every pair's q8 values and of every row's
+                // codes (with lane groups on values {0, 16, 8, 24}[kq] the pair
+                // reads of a half-wave fell on half the banks twice: ~1.0M
+                // conflict cycles per c5 64-token launch, now ~1K, the stage
+                // time unchanged); per block the reference's sumf +=
+                // scale_half(e) * sumi for sumi != 0 (an fma of a power of two
+                // and an int < 2^24 is exact, and sumi = 0 adds +0 to a sum
+                // that is never -0), then yd * sumf
+                const uint32_t nsh = 4u * (kq >> 1), a_piece = kq, w_piece = kq & 1u;
                 const uint32_t nb = lim - 8u * sb < 8u ? lim - 8u * sb : 8u;
                 uint2 ev[NM];
                 float f[NM][4];
@@ -989,7 +994,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                     const uint2 a = *(const uint2 *)(rec + 16u + 32u * bl + 8u * a_piece);
 #pragma unroll
                     for (uint32_t mt = 0; mt < NM; mt++) {
-                        const uint2 qq = *(const uint2 *)(ws + mt * 16u * kRowL + 16u * bl + 8u * (kq >> 1));
+                        const uint2 qq = *(const uint2 *)(ws + mt * 16u * kRowL + 16u * bl + 8u * w_piece);
                         const v4i d = mfma16x16x32(a, make_uint2(mxfp4_kv4(qq.x >> nsh), mxfp4_kv4(qq.y >> nsh)));
                         const float sc = mxfp4_scale_half(byte_of(ev[mt], bl));
                         for (int r = 0; r < 4; r++) f[mt][r] = __builtin_fmaf(sc, (float)d[r], f[mt][r]);
