@@ -16,7 +16,7 @@ from pulsar_amd import formats as fm
 from pulsar_amd import kernels as K
 from pulsar_amd import synth
 from pulsar_amd.formats import (ACT_SILU, ACT_SWIGLU_OAI, QUANT_IQ2_XXS, QUANT_MXFP4, QUANT_Q2_K, QUANT_Q4_K,
-                                QUANT_Q6_K, row_bytes)
+                                QUANT_Q6_K, q8k_blocks, row_bytes)
 from tests.gpu_util import TOL_REL, down, up, up_f32, zeros_f32
 
 pytestmark = pytest.mark.gpu
@@ -489,6 +489,29 @@ def test_matmul_f32_and_bias(dev):
         before = down(out)
         K.add_bias_rows(out, up_f32(b), out_dim, n_tok)
         assert np.array_equal(down(out), oracle.add_bias_rows(before, b, out_dim, n_tok))
+
+
+@pytest.mark.parametrize("out_dim", [8, 12, 16, 24, 32, 40, 64, 100, 128, 136, 256])
+def test_gemv_block_order_every_split(dev, out_dim):
+    """The router GEMV's blocks are ordered over the 8 XCDs by a row x token-
+    group split chosen per shape (none, or 2 / 4 / 8 row bands): every
+    (row, token) output must come out once, equal to the oracle's, for token
+    counts that give every split and group counts that divide it or not, and
+    the fused router's logits bit-identical to matmul_f32's."""
+    in_dim = 96
+    wt = (rng.standard_normal((out_dim, in_dim)) / np.sqrt(in_dim)).astype(np.float32)
+    for n_tok in (1, 2, 5, 8, 16, 17, 32, 33, 64, 128):
+        x = rng.standard_normal((n_tok, in_dim)).astype(np.float32)
+        out = torch.full((n_tok, out_dim), float("nan"), dtype=torch.float32, device=dev)
+        K.matmul_f32(out, up_f32(wt), up_f32(x), in_dim, out_dim, n_tok)
+        want = oracle.matmul_f32(wt, x, in_dim, out_dim, n_tok)
+        got = down(out)
+        scale = np.abs(x) @ np.abs(wt).T
+        assert (np.abs(got - want) <= 1e-6 * scale + 1e-30).all(), (out_dim, n_tok)
+        logits = torch.full((n_tok, out_dim), float("nan"), dtype=torch.float32, device=dev)
+        xq = torch.zeros(n_tok * q8k_blocks(in_dim) * 292, dtype=torch.uint8, device=dev)
+        K.router_logits_q8(logits, xq, up_f32(x), up_f32(wt), None, in_dim, out_dim, n_tok)
+        assert np.array_equal(down(logits).view(np.uint32), got.view(np.uint32)), (out_dim, n_tok)
 
 
 # ------------------------------------------------- device routing, graphs --
