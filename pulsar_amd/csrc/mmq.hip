@@ -891,15 +891,13 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             tv[j] = F::kTailBytes == 4u ? ldw32(tp) : F::kTailBytes == 2u ? (uint32_t)ldw16(tp) : ldw8(tp);
         }
     };
-    // MXFP4 (both stages), the IQ2_XXS down stage and the Q2_K gate / up
-    // stage request their first step of weights before the pair tile's
-    // activations are staged, so the two round trips overlap (alternating
-    // libraries: c5 64-token layer 162.4 -> 160.5 us, gate / up 94.9 ->
-    // 93.4, down 49.3 -> 48.5; c4 IQ2_XXS down 53.9 -> 52.8 us; c4 Q2_K gate
-    // / up 77.9 -> 77.5 us, layer medians 139.4 -> 138.9 us over five
-    // rounds). The Q2_K down stage is slower that way (c4 45.7 -> 46.5 us)
-    // and IQ2_XXS gate / up is unchanged.
-    constexpr bool kEarly = kMx || (kIq2 && !PAIR) || (Q == PULSAR_QUANT_Q2_K && PAIR);
+    // MXFP4 (both stages) and the IQ2_XXS down stage request their first
+    // step of weights before the pair tile's activations are staged, so the
+    // two round trips overlap (alternating libraries: c5 64-token layer
+    // 162.4 -> 160.5 us, gate / up 94.9 -> 93.4, down 49.3 -> 48.5; c4
+    // IQ2_XXS down 53.9 -> 52.8 us). The Q2_K stages are slower that way
+    // (c4 down 45.7 -> 46.5 us) and IQ2_XXS gate / up is unchanged.
+    constexpr bool kEarly = kMx || (kIq2 && !PAIR);
     if (kEarly && active) issue(0u, 0u);
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
