@@ -185,7 +185,8 @@ def moe_route(selected, weights, ptrs, slot_weights, active, logits, router_bias
               weight_scale: float, softmax_mode: int, bank: "ExpertBank", shared, n_tok: int) -> None:
     """router_select (modes 0/1) + moe_route_ptrs in one launch (equal
     outputs), plus `active` (uint32 [2 + n_expert]): the count of distinct
-    selected experts, the count of NULL slots, the expert ids ascending."""
+    selected experts, the count of NULL slots, the expert ids in order of
+    first appearance in (token, slot) order."""
     arr, n_shared = _shared_array(shared)
     _check(_lib.load().pulsar_moe_route(
         _ptr(selected), _ptr(weights), _ptr(ptrs), _ptr(slot_weights), _ptr(active), _ptr(logits), _ptr(router_bias),

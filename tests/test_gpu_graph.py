@@ -123,6 +123,74 @@ def test_fused_and_grouped_chains_capture(dev):
                                                                n_tok) or other.zero_())
 
 
+def test_expert_chain_replays_follow_new_inputs(dev):
+    """The expert-indexed chunk layer (router_logits_q8 -> moe_route ->
+    experts gate / up -> quantize -> experts down -> slot sum), captured once
+    and replayed on new activations copied into the captured input: the
+    routing, the count of touched experts and the groups change from replay
+    to replay inside the same graph (its grids are sized for the most
+    groups; blocks past the count exit), and each replay must equal an eager
+    run of the chain on the same input bit for bit. One input sends every
+    token to the same experts (k groups), another spreads them."""
+    hidden, ffn, E, k, n_tok = 512, 256, 24, 4, 12
+    L = Layer(QUANT_Q2_K, QUANT_Q2_K, hidden=hidden, ffn=ffn, E=E, n_used=k, n_tok=1)
+    bank = _bank(L)
+    f32 = dict(dtype=torch.float32, device=dev)
+    x = torch.zeros((n_tok, hidden), **f32)
+    wr = up_f32((rng.standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32))
+    nb_in, nb_mid = q8k_blocks(hidden), q8k_blocks(ffn)
+    b = dict(logits=torch.zeros((n_tok, E), **f32),
+             xq=torch.zeros(n_tok * nb_in * 292, dtype=torch.uint8, device=dev),
+             sel=torch.zeros((n_tok, k), dtype=torch.int32, device=dev),
+             rw=torch.zeros((n_tok, k), **f32),
+             ptrs=torch.zeros(n_tok * k * 48, dtype=torch.uint8, device=dev),
+             slot_w=torch.zeros((n_tok, k), **f32),
+             active=torch.zeros(2 + E, dtype=torch.int32, device=dev),
+             mid=torch.zeros((n_tok * k, ffn), **f32),
+             midq=torch.zeros(n_tok * k * nb_mid * 292, dtype=torch.uint8, device=dev),
+             partial=torch.zeros((n_tok * k, hidden), **f32),
+             out=torch.zeros((n_tok, hidden), **f32))
+
+    def chain():
+        K.router_logits_q8(b["logits"], b["xq"], x, wr, None, hidden, E, n_tok)
+        K.moe_route(b["sel"], b["rw"], b["ptrs"], b["slot_w"], b["active"], b["logits"], None, E, k, 1.0, 1, bank,
+                    None, n_tok)
+        K.moe_pair_swiglu_experts(b["mid"], b["sel"], b["active"], b["slot_w"], b["xq"], bank, E, None, n_tok, k,
+                                  hidden, ffn, L.grb, QUANT_Q2_K, ACT_SILU)
+        K.quantize_q8_k(b["midq"], b["mid"], ffn, n_tok * k)
+        K.moe_down_experts(b["partial"], b["sel"], b["active"], b["midq"], bank, E, None, n_tok, k, ffn, hidden,
+                           L.drb, QUANT_Q2_K)
+        K.moe_slot_sum(b["out"], b["partial"], hidden, k, n_tok)
+
+    x.copy_(up_f32(rng.standard_normal((n_tok, hidden)).astype(np.float32)))
+    chain()
+    runtime.sync()
+    g = runtime.Graph.capture(chain)
+    one = rng.standard_normal(hidden).astype(np.float32)
+    inputs = [rng.standard_normal((n_tok, hidden)).astype(np.float32),
+              np.tile(one, (n_tok, 1)),  # every token on the same k experts
+              (rng.standard_normal((n_tok, hidden)) * 3.0).astype(np.float32)]
+    counts = []
+    for xi in inputs:
+        x.copy_(up_f32(xi))
+        for t in b.values():
+            t.zero_()
+        torch.cuda.synchronize()
+        g.launch()
+        runtime.sync()
+        got = {name: down(t).copy() for name, t in b.items()}
+        for t in b.values():
+            t.zero_()
+        torch.cuda.synchronize()
+        chain()
+        runtime.sync()
+        for name, t in b.items():
+            assert np.array_equal(got[name].view(np.uint8), down(t).view(np.uint8)), name
+        counts.append(int(got["active"][0]))
+        assert np.abs(got["out"]).max() > 0
+    assert counts[1] == k and counts[0] > k, counts
+
+
 def test_set_stream_none_restores_per_thread_default(dev):
     """pulsar_set_stream(NULL) routes launches back to the per-thread default
     stream: a capture begun there records them."""
