@@ -736,12 +736,13 @@ constexpr uint32_t kGqWaves = Q == PULSAR_QUANT_MXFP4 ? 12u : 4u;
 // stages (c5 64 tokens: gate / up 112.3 -> 97.5 us, its 2880 rows in 8
 // blocks of 384 so the 32 experts' blocks make one round of 256 blocks,
 // one per CU; down 56.9 -> 51.9 us; 3 and 4 leave CUs idle in the down
-// stage, 64 / 81 us); IQ2_XXS down 2 (c4 60.5 -> 57.0 us); 1 for the
-// others: Q2_K down 50.2 at 1, 50.1 / 49.4 / 51.9 at 2 / 3 / 4, and two
-// tiles in the K-quant gate / up stages cost them occupancy or block
-// count (c4 Q2_K 85.3 -> 92.0 us, IQ2_XXS 104.5 -> 150.2 us).
+// stage, 64 / 81 us); IQ2_XXS down 2 (c4 60.5 -> 57.0 us); Q2_K down 2
+// with its first step requested before the staging (c4 44.8 -> 43.7 us;
+// either change alone measured within noise or slower); 1 for the
+// others: two tiles in the K-quant gate / up stages cost them occupancy or
+// block count (c4 Q2_K 85.3 -> 92.0 us, IQ2_XXS 104.5 -> 150.2 us).
 template <uint32_t Q, bool PAIR>
-constexpr uint32_t kGqTiles = Q == PULSAR_QUANT_MXFP4 ? 2u : (Q == PULSAR_QUANT_IQ2_XXS && !PAIR) ? 2u : 1u;
+constexpr uint32_t kGqTiles = Q == PULSAR_QUANT_MXFP4 ? 2u : ((Q == PULSAR_QUANT_IQ2_XXS || Q == PULSAR_QUANT_Q2_K) && !PAIR) ? 2u : 1u;
 template <uint32_t Q, bool PAIR>
 constexpr uint32_t kGqBlockRows = 16u * kGqWaves<Q> * kGqTiles<Q, PAIR>;
 
@@ -891,13 +892,16 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
             tv[j] = F::kTailBytes == 4u ? ldw32(tp) : F::kTailBytes == 2u ? (uint32_t)ldw16(tp) : ldw8(tp);
         }
     };
-    // MXFP4 (both stages) and the IQ2_XXS down stage request their first
-    // step of weights before the pair tile's activations are staged, so the
-    // two round trips overlap (alternating libraries: c5 64-token layer
-    // 162.4 -> 160.5 us, gate / up 94.9 -> 93.4, down 49.3 -> 48.5; c4
-    // IQ2_XXS down 53.9 -> 52.8 us). The Q2_K stages are slower that way
-    // (c4 down 45.7 -> 46.5 us) and IQ2_XXS gate / up is unchanged.
-    constexpr bool kEarly = kMx || (kIq2 && !PAIR);
+    // MXFP4 (both stages) and the IQ2_XXS and Q2_K down stages request
+    // their first step of weights before the pair tile's activations are
+    // staged, so the two round trips overlap (alternating libraries: c5
+    // 64-token layer 162.4 -> 160.5 us, gate / up 94.9 -> 93.4, down 49.3 ->
+    // 48.5; c4 IQ2_XXS down 53.9 -> 52.8 us; c4 Q2_K down, with two row
+    // tiles per wave, 44.8 -> 43.7 us, though it then fetches ~9% more: the
+    // lines its first two steps share leave the L2 while the staging runs).
+    // The Q2_K gate / up stage fetched 5% more that way for no measurable
+    // gain, and IQ2_XXS gate / up is unchanged.
+    constexpr bool kEarly = kMx || ((kIq2 || Q == PULSAR_QUANT_Q2_K) && !PAIR);
     if (kEarly && active) issue(0u, 0u);
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
