@@ -862,12 +862,14 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     const uint32_t act_bytes = act_row_pitch(k_blocks);
     uint4 wv[kWj];
     uint32_t tv[kTjA];
-    auto issue = [&](uint32_t tile, uint32_t step) {
+    auto issue = [&](uint32_t tile, uint32_t step, bool adv) {
         // a new row tile: the pieces' step-0 addresses move 16 rows on
         // (the tile before it was whole), or are formed again with the
         // rows clamped when the tile ends past the matrix (wave-uniform
-        // branches, no loads under them)
-        if (T > 1u && step == 0u && tile > 0u) {
+        // branches, no loads under them). adv = false: the walk's last
+        // (tile, step) requested again past the end (one-step rows), whose
+        // addresses are the current ones and must not move on
+        if (T > 1u && adv && step == 0u && tile > 0u) {
             if (rw0 + 16u * tile + 16u <= n_rows) {
 #pragma unroll
                 for (uint32_t j = 0; j < kWj; j++) wsrc[j] += 16u * row_bytes;
@@ -902,7 +904,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
     // The Q2_K gate / up stage fetched 5% more that way for no measurable
     // gain, and IQ2_XXS gate / up is unchanged.
     constexpr bool kEarly = kMx || ((kIq2 || Q == PULSAR_QUANT_Q2_K) && !PAIR);
-    if (kEarly && active) issue(0u, 0u);
+    if (kEarly && active) issue(0u, 0u, true);
     for (uint32_t t0 = s0; t0 < s1; t0 += pmax) {
         const uint32_t m = s1 - t0 < pmax ? s1 - t0 : pmax;
         if (t0 != s0) __syncthreads();  // the previous tile's activations are consumed
@@ -1256,7 +1258,7 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
 #pragma unroll
             for (uint32_t j = 0; j < kTj; j++) tsrc[j] = tsrc_at(j, 0u);
         }
-        if (!kEarly || t0 != s0) issue(0u, 0u);
+        if (!kEarly || t0 != s0) issue(0u, 0u, true);
         // (tile, step) in order; the next one's loads are in flight while
         // this one is decoded (past the last, the last again: never stored)
         const uint32_t tiles = T == 1u ? 1u : n_tiles;
@@ -1281,11 +1283,12 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 uint32_t nt = tile, ns = step + 1u;
+                const bool more = ns < n_steps || tile + 1u < tiles;
                 if (ns == n_steps) {
                     ns = tile + 1u < tiles ? 0u : step;
                     nt = tile + 1u < tiles ? tile + 1u : tile;
                 }
-                issue(nt, ns);
+                issue(nt, ns, more);
 #pragma unroll
                 for (uint32_t sl = 0; sl < S; sl++)
                     if (step * S + sl < k_blocks)
@@ -1324,11 +1327,12 @@ __global__ __launch_bounds__(64 * kGqWaves<Q>) __attribute__((amdgpu_waves_per_e
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 uint32_t nt = tile, ns = step + 1u;
+                const bool more = ns < n_steps || tile + 1u < tiles;
                 if (ns == n_steps) {
                     ns = tile + 1u < tiles ? 0u : step;
                     nt = tile + 1u < tiles ? tile + 1u : tile;
                 }
-                issue(nt, ns);
+                issue(nt, ns, more);
 #pragma unroll
                 for (uint32_t sl = 0; sl < S; sl++)
                     if (step * S + sl < k_blocks)
