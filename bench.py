@@ -656,7 +656,7 @@ def pmc_run(ctx, which: str):
         dn = d * s.hidden * s.down_row_bytes
         router = s.n_expert * s.hidden * 4 + s.n_tok * s.hidden * 4 + s.n_tok * s.n_expert * 4 + s.n_tok * nb_in * 292
         if path == "grouped":
-            alg = {f"pk::router_logits_q8_kernel<4u>": router,
+            alg = {f"pk::router_logits_q8_kernel<2u>": router,
                    f"pk::moe_grouped_mmq_kq_kernel<{s.gate_quant}u, true, pk::ExpertGroups>":
                        gu + n_pairs * nb_in * 292 + n_pairs * s.ffn * 4,
                    f"pk::moe_grouped_mmq_kq_kernel<{s.down_quant}u, false, pk::ExpertGroups>":

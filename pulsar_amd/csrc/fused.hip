@@ -342,7 +342,7 @@ extern "C" int pulsar_router_logits_q8(void *logits, void *xq, const void *x, co
                                        uint32_t in_dim, uint32_t n_expert, uint32_t n_tok) {
     if (!logits || !xq || !x || !w_r || in_dim == 0 || n_expert == 0 || n_tok == 0)
         return reject("router logits q8");
-    const uint32_t tg = n_tok == 1u ? 1u : 4u;
+    const uint32_t tg = n_tok == 1u ? 1u : 2u;
     const uint64_t work = (uint64_t)n_expert * ((n_tok + tg - 1u) / tg);
     const uint32_t nb = (in_dim + 255u) / 256u;
     const uint64_t qblocks = ((uint64_t)n_tok * nb + 3u) / 4u;
@@ -355,7 +355,7 @@ extern "C" int pulsar_router_logits_q8(void *logits, void *xq, const void *x, co
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
                            in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb, rbl);
     else
-        hipLaunchKernelGGL(router_logits_q8_kernel<4>, grid, dim3(256), 0, pk::stream(), (float *)logits,
+        hipLaunchKernelGGL(router_logits_q8_kernel<2>, grid, dim3(256), 0, pk::stream(), (float *)logits,
                            (pulsar_block_q8_K *)xq, (const float *)x, (const float *)w_r, (const float *)bias,
                            in_dim, n_expert, n_tok, (uint32_t)gemv_blocks, nb, rbl);
     return launch_ok("router logits q8 launch");
